@@ -1,0 +1,153 @@
+/*
+ * pagedattn.h -- C ABI of the MI355X (gfx950) paged-KV grouped-query decode
+ * attention library `libpagedattn_hip.so`.
+ *
+ * The reference project has no native ABI: its host wrapper launches two
+ * Triton kernels directly. Each entry point below replaces one of those
+ * launches (citations are into ParamThakkar123/paged-decode-attention):
+ *
+ *   pa_decode        <- `_paged_decode_kernel[grid](...)` and, when
+ *                       num_splits > 1, the `_split_reduce_kernel[grid](...)`
+ *                       launch that follows it
+ *                       (pagedattn/triton_decode.py:331-376)
+ *   pa_split_reduce  <- `_split_reduce_kernel[(b, hq)](...)` on its own
+ *                       (pagedattn/triton_decode.py:198-240, 368-376)
+ *
+ * Everything is plain C: device pointers, sizes, element strides and enums.
+ * No function throws; each returns PA_OK (0) or a negative PA_ERR_* code and
+ * records a message readable through pa_last_error() on the same thread.
+ * Arguments are validated before any HIP call, so validation is testable on
+ * a machine without a GPU. Launches are asynchronous on the stream passed in
+ * (a hipStream_t, passed as void*; NULL means the legacy default stream).
+ * The library allocates no device memory: the caller owns every buffer,
+ * including the split-KV workspace (part_out / part_lse).
+ *
+ * Tensor layouts (element strides; the innermost dimension is contiguous):
+ *   q          [batch, num_q_heads, head_dim]                  fp16
+ *   k_cache    [num_blocks, block_size, num_kv_heads, head_dim] fp16 | fp8_e5m2 | int8
+ *   v_cache    same shape and strides as k_cache
+ *   k_scale    [num_blocks, block_size, num_kv_heads]           fp16 | fp32 (int8 only)
+ *   v_scale    same shape and strides as k_scale
+ *   out        [batch, num_q_heads, head_dim]                  fp16
+ *   part_out   [batch, num_q_heads, num_splits, head_dim]      fp32
+ *   part_lse   [batch, num_q_heads, num_splits]                fp32, log2 domain
+ *   block_table[batch, max_blocks]                             int32
+ *   seq_lens   [batch]                                         int32
+ */
+#ifndef PAGEDATTN_H_
+#define PAGEDATTN_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PA_ABI_VERSION 1
+
+/* Return codes. */
+#define PA_OK 0
+#define PA_ERR_INVALID (-1)     /* bad pointer, size, stride or enum */
+#define PA_ERR_UNSUPPORTED (-2) /* valid but not built (e.g. head_dim 96) */
+#define PA_ERR_HIP (-3)         /* a HIP runtime call failed */
+
+/* KV cache element type: the reference's `_KV_CODE`
+ * (pagedattn/triton_decode.py:30) with fp16 = 0, fp8_e5m2 = 1, int8 = 2. */
+#define PA_KV_FP16 0
+#define PA_KV_FP8_E5M2 1 /* OCP e5m2 (torch.float8_e5m2), not the FNUZ variant */
+#define PA_KV_INT8 2
+
+/* Per-(token, kv_head) dequantization scale type (int8 KV only). */
+#define PA_SCALE_NONE 0
+#define PA_SCALE_FP16 1 /* the reference's choice (pagedattn/cache.py:45) */
+#define PA_SCALE_FP32 2
+
+/* q / out element type. */
+#define PA_IO_FP16 0
+
+/* Largest supported split count and GQA group handled in one pass. */
+#define PA_MAX_SPLITS 4096
+#define PA_MAX_GROUP 16
+
+typedef struct pa_decode_args {
+  /* device pointers */
+  const void *q;
+  const void *k_cache;
+  const void *v_cache;
+  const void *k_scale; /* int8 only; NULL otherwise */
+  const void *v_scale; /* int8 only; NULL otherwise */
+  void *out;
+  float *part_out; /* num_splits > 1 only; NULL otherwise */
+  float *part_lse; /* num_splits > 1 only; NULL otherwise */
+  const int32_t *block_table;
+  const int32_t *seq_lens;
+  /* sizes */
+  int32_t batch;
+  int32_t num_q_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;   /* 32, 64, 128 or 256 */
+  int32_t block_size; /* page size in tokens: 16, 32, 64, 128 or 256 */
+  int32_t num_blocks; /* pool size; block-table entries are clamped into it */
+  int32_t max_blocks; /* block_table row length */
+  int32_t num_splits; /* >= 1; > 1 selects the split-KV two-pass path */
+  /* element strides */
+  int64_t stride_qb, stride_qh;
+  int64_t stride_kn, stride_kt, stride_kh; /* shared by k_cache and v_cache */
+  int64_t stride_sn, stride_st;            /* shared by k_scale and v_scale */
+  int64_t stride_ob, stride_oh;
+  int64_t stride_pb, stride_ph, stride_ps; /* part_out */
+  int64_t stride_lb, stride_lh;            /* part_lse */
+  int64_t stride_btb;
+  /* types and scalars */
+  int32_t kv_dtype;    /* PA_KV_* */
+  int32_t scale_dtype; /* PA_SCALE_* */
+  int32_t io_dtype;    /* PA_IO_* */
+  float sm_scale;      /* softmax scale applied to q.k (natural-log domain) */
+} pa_decode_args;
+
+typedef struct pa_reduce_args {
+  const float *part_out; /* [batch, num_heads, num_splits, head_dim] */
+  const float *part_lse; /* [batch, num_heads, num_splits], log2 domain */
+  void *out;             /* [batch, num_heads, head_dim] */
+  int32_t batch;
+  int32_t num_heads;
+  int32_t head_dim;
+  int32_t num_splits;
+  int64_t stride_pb, stride_ph, stride_ps;
+  int64_t stride_lb, stride_lh;
+  int64_t stride_ob, stride_oh;
+  int32_t io_dtype; /* PA_IO_* */
+} pa_reduce_args;
+
+/* Paged GQA decode attention for one query token per sequence.
+ * out[b, h, :] = softmax(sm_scale * q[b, h] . K[b, h / group, 0:T_b]) V[...]
+ * with T_b = seq_lens[b] and group = num_q_heads / num_kv_heads.
+ * num_splits == 1: one kernel writes `out` directly.
+ * num_splits  > 1: the decode kernel writes per-split partials (normalised
+ * output and log2-sum-exp) into part_out / part_lse, then the reduce kernel
+ * merges them into `out`. A sequence with T_b == 0 yields zeros (the
+ * reference yields NaN there). Replaces pagedattn/triton_decode.py:331-376. */
+int pa_decode(const pa_decode_args *args, void *stream);
+
+/* Decode pass only: writes part_out / part_lse (num_splits >= 1) and skips
+ * the merge, so a caller can time or distribute the passes separately.
+ * Replaces the `_paged_decode_kernel[(b, hkv, num_splits)]` launch
+ * (pagedattn/triton_decode.py:351-367). */
+int pa_decode_partials(const pa_decode_args *args, void *stream);
+
+/* Merge of split partials: out = sum_s part_s * 2^(lse_s - m) /
+ * sum_s 2^(lse_s - m), m = max_s lse_s; all-empty rows yield zeros.
+ * Replaces pagedattn/triton_decode.py:198-240 / 368-376. */
+int pa_split_reduce(const pa_reduce_args *args, void *stream);
+
+/* Message for the last non-zero return on the calling thread ("" if none). */
+const char *pa_last_error(void);
+
+/* PA_ABI_VERSION of the built library. */
+int pa_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PAGEDATTN_H_ */

@@ -1,0 +1,226 @@
+"""CPU oracle for paged GQA decode attention -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+import this module, and only as the checker. The product
+(paged-decode-attention_amd/) never imports it and has no CPU path.
+
+A from-scratch restatement, in torch on the CPU, of the reference's algorithm
+(ParamThakkar123/paged-decode-attention):
+
+  quantize_kv        pagedattn/cache.py:33-48
+  dequantize_kv      pagedattn/cache.py:51-62
+  gather_contiguous  pagedattn/cache.py:187-215
+  reference_decode   pagedattn/reference.py:28-49
+  split_partials     pagedattn/triton_decode.py:78-85 (per-split KV range) and
+                     :169-188 (normalised partial + log2-sum-exp, empty = -inf)
+  split_merge        pagedattn/triton_decode.py:198-240
+  sdpa_math_decode   pagedattn/reference.py:57-72 (SDPA math backend, GQA)
+
+Deviations, each deliberate: `reference_decode` takes `sm_scale` (the
+reference always uses head_dim**-0.5, reference.py:45) and can return the
+fp32 result before the final cast (`out_dtype=torch.float32`); the reference
+casts to q.dtype (reference.py:49). Everything works on any object carrying
+the PagedKVCache field names (shape, block_size, kv_dtype, k_cache, v_cache,
+k_scale, v_scale, block_table, seq_lens), so this module does not import the
+product package.
+
+How each function is pinned (tests/test_oracle.py): an independent float64
+C implementation that walks the pages directly (oracle/pa_oracle.c), closed
+forms (T=1, q=0, constant V, a dominant logit), torch SDPA's math backend on
+the gathered cache, block-table permutation invariance, e5m2 bit identities
+and int8 round-trip bounds, and the golden fixtures under tests/golden/.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+INT8_MAX = 127.0
+
+
+def quantize_kv(x: torch.Tensor, kv_dtype: str, scale_dtype: torch.dtype = torch.float16):
+    """fp16 [..., H, D] -> (stored, scale or None). cache.py:33-48."""
+    if kv_dtype == "fp16":
+        return x.to(torch.float16), None
+    if kv_dtype == "bf16":
+        return x.to(torch.bfloat16), None
+    if kv_dtype == "fp8_e5m2":
+        return x.to(torch.float8_e5m2), None
+    if kv_dtype == "int8":
+        amax = x.abs().amax(dim=-1, keepdim=True).float().clamp_min(1e-6)
+        scale = (amax / INT8_MAX).to(scale_dtype)
+        q = torch.round(x.float() / scale.float()).clamp(-INT8_MAX, INT8_MAX).to(torch.int8)
+        return q, scale.squeeze(-1)
+    raise ValueError(f"unknown kv_dtype {kv_dtype}")
+
+
+def dequantize_kv(q: torch.Tensor, scale: torch.Tensor | None, kv_dtype: str) -> torch.Tensor:
+    """Stored KV -> fp16. cache.py:51-62.
+
+    int8: the product int8 * scale is formed in fp32 and rounded once to fp16.
+    With an fp16 scale this equals the reference's fp16 multiply (the product
+    of an 8-bit integer and an 11-bit significand is exact in fp32).
+    """
+    if kv_dtype in ("fp16", "bf16", "fp8_e5m2"):
+        return q.to(torch.float16)
+    if kv_dtype == "int8":
+        assert scale is not None
+        return (q.float() * scale.float().unsqueeze(-1)).to(torch.float16)
+    raise ValueError(f"unknown kv_dtype {kv_dtype}")
+
+
+def gather_contiguous(cache) -> tuple[torch.Tensor, torch.Tensor]:
+    """Dense [B, H_kv, S_max, D] fp16 K and V. cache.py:187-215.
+
+    Positions past a sequence's last page read the page-table entry clamped to
+    the last column (padding rows); the caller masks them.
+    """
+    bt = cache.block_table.cpu().long()
+    lens = cache.seq_lens.cpu().long()
+    b = bt.shape[0]
+    s_max = int(lens.max().item()) if b else 0
+    bs = cache.block_size
+    pos = torch.arange(s_max)
+    blk = (pos // bs).clamp(max=bt.shape[1] - 1)
+    off = pos % bs
+    phys = bt[:, blk]  # [B, S]
+    offs = off.unsqueeze(0).expand(b, -1)
+    out = []
+    for cache_t, scale_t in ((cache.k_cache, cache.k_scale), (cache.v_cache, cache.v_scale)):
+        c = cache_t.cpu()
+        flat = c[phys, offs]  # [B, S, H, D]
+        s = scale_t.cpu()[phys, offs] if scale_t is not None else None
+        flat = dequantize_kv(flat, s, cache.kv_dtype)
+        out.append(flat.permute(0, 2, 1, 3).contiguous())
+    return out[0], out[1]
+
+
+def _softmax_scale(cache, sm_scale: float | None) -> float:
+    return cache.shape.head_dim ** -0.5 if sm_scale is None else float(sm_scale)
+
+
+def reference_decode(
+    q: torch.Tensor,
+    cache,
+    sm_scale: float | None = None,
+    out_dtype: torch.dtype | None = None,
+) -> torch.Tensor:
+    """fp32 paged GQA decode attention on the CPU. reference.py:28-49.
+
+    q: [B, H_q, D] -> [B, H_q, D] in `out_dtype` (default q.dtype). Query head
+    h reads kv head h // group. A sequence of length 0 gives NaN, as in the
+    reference (softmax over an all -inf row).
+    """
+    qc = q.cpu()
+    b, hq, d = qc.shape
+    hkv = cache.shape.num_kv_heads
+    group = hq // hkv
+    k, v = gather_contiguous(cache)
+    k = k.float()
+    v = v.float()
+    qf = qc.float()
+    s_max = k.shape[2]
+    lens = cache.seq_lens.cpu().long()
+    valid = torch.arange(s_max).unsqueeze(0) < lens.unsqueeze(1)  # [B, S]
+    scale = _softmax_scale(cache, sm_scale)
+    out = torch.empty((b, hq, d), dtype=torch.float32)
+    for h in range(hq):
+        kvh = h // group
+        logits = torch.einsum("bd,bsd->bs", qf[:, h], k[:, kvh]) * scale
+        logits = logits.masked_fill(~valid, float("-inf"))
+        p = torch.softmax(logits, dim=-1)
+        out[:, h] = torch.einsum("bs,bsd->bd", p, v[:, kvh])
+    return out.to(q.dtype if out_dtype is None else out_dtype)
+
+
+def split_ranges(seq_len: int, num_splits: int, align: int) -> list[tuple[int, int]]:
+    """[lo, hi) of each split: chunk = ceil(ceil(T/align)/S)*align.
+    triton_decode.py:78-85 with the alignment unit as a parameter."""
+    chunk = -(-(-(-seq_len // align)) // num_splits) * align
+    out = []
+    for s in range(num_splits):
+        lo = s * chunk
+        out.append((lo, min(lo + chunk, seq_len)))
+    return out
+
+
+def split_partials(
+    q: torch.Tensor,
+    cache,
+    num_splits: int,
+    align: int = 32,
+    sm_scale: float | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-split normalised output [B, Hq, S, D] and log2-sum-exp [B, Hq, S].
+
+    For split s over tokens [lo, hi): with x_j = q.k_j * scale * log2(e),
+    lse = log2(sum_j 2^x_j) and out = sum_j 2^(x_j - lse) v_j; an empty split
+    has lse = -inf and out = 0 (triton_decode.py:169-188).
+    """
+    qc = q.cpu().float()
+    b, hq, d = qc.shape
+    hkv = cache.shape.num_kv_heads
+    group = hq // hkv
+    k, v = gather_contiguous(cache)
+    k = k.float()
+    v = v.float()
+    scale = _softmax_scale(cache, sm_scale) * math.log2(math.e)
+    lens = cache.seq_lens.cpu().long().tolist()
+    part = torch.zeros((b, hq, num_splits, d), dtype=torch.float32)
+    lse = torch.full((b, hq, num_splits), float("-inf"), dtype=torch.float32)
+    for bi in range(b):
+        for s, (lo, hi) in enumerate(split_ranges(lens[bi], num_splits, align)):
+            if lo >= hi:
+                continue
+            for h in range(hq):
+                kvh = h // group
+                x = (k[bi, kvh, lo:hi] @ qc[bi, h]) * scale  # [n]
+                m = x.max()
+                w = torch.exp2(x - m)
+                den = w.sum()
+                part[bi, h, s] = (w @ v[bi, kvh, lo:hi]) / den
+                lse[bi, h, s] = m + torch.log2(den)
+    return part, lse
+
+
+def split_merge(part: torch.Tensor, lse: torch.Tensor) -> torch.Tensor:
+    """out = sum_s part_s 2^(lse_s - m) / sum_s 2^(lse_s - m). triton_decode.py:221-240.
+    Returns fp32 [B, H, D]; rows whose splits are all empty give NaN (0/0),
+    as the reference does."""
+    m = lse.max(dim=-1, keepdim=True).values
+    w = torch.exp2(lse - m)
+    w = torch.where(torch.isfinite(lse), w, torch.zeros_like(w))
+    return (part * w.unsqueeze(-1)).sum(dim=2) / w.sum(dim=-1, keepdim=True)
+
+
+def sdpa_math_decode(q: torch.Tensor, cache, sm_scale: float | None = None) -> torch.Tensor:
+    """torch SDPA (math backend, enable_gqa) on the gathered cache, fp32.
+    The library cross-check of reference.py:57-72 / tests/test_correctness.py:118-122."""
+    import torch.nn.functional as F
+
+    k, v = gather_contiguous(cache)
+    qf = q.cpu().float().unsqueeze(2)  # [B, Hq, 1, D]
+    lens = cache.seq_lens.cpu().long()
+    s = k.shape[2]
+    mask = (torch.arange(s).view(1, 1, 1, -1) < lens.view(-1, 1, 1, 1))
+    with torch.nn.attention.sdpa_kernel(torch.nn.attention.SDPBackend.MATH):
+        o = F.scaled_dot_product_attention(
+            qf, k.float(), v.float(), attn_mask=mask,
+            enable_gqa=(qf.shape[1] != k.shape[1]),
+            scale=_softmax_scale(cache, sm_scale),
+        )
+    return o.squeeze(2)
+
+
+def bytes_read_per_decode_step(cache) -> int:
+    """K/V (+ scale) bytes inside the sequences. cache.py:90-102, with the
+    scale counted at its real element size."""
+    n_tok = int(cache.seq_lens.cpu().long().sum().item())
+    h, d = cache.shape.num_kv_heads, cache.shape.head_dim
+    elem = cache.k_cache.element_size()
+    total = 2 * n_tok * h * d * elem
+    if cache.kv_dtype == "int8":
+        total += 2 * n_tok * h * cache.k_scale.element_size()
+    return total

@@ -1,0 +1,26 @@
+"""Paged-KV GQA decode attention for MI355X (gfx950), HIP kernels behind a C ABI.
+
+Public surface of the reference package (ParamThakkar123/paged-decode-attention,
+pagedattn/__init__.py:3-13) restricted to the decode path: shapes, the paged
+cache, the decode entry point and the split heuristic. The reference's fp32
+oracle and dense SDPA baselines are test infrastructure here and live outside
+the package (oracle/).
+"""
+
+from .config import LLAMA3_8B, LLAMA3_70B, MHA_DEBUG, QWEN25_05B, KVDType, ModelShape, kv_bytes_per_token
+from .cache import PagedKVCache, allocate, quantize_kv
+from .hip_decode import (
+    decode_partials,
+    paged_decode_hip,
+    paged_decode_triton,
+    pick_num_splits,
+    split_reduce,
+)
+
+__all__ = [
+    "LLAMA3_8B", "LLAMA3_70B", "MHA_DEBUG", "QWEN25_05B", "KVDType", "ModelShape",
+    "kv_bytes_per_token",
+    "PagedKVCache", "allocate", "quantize_kv",
+    "paged_decode_hip", "paged_decode_triton", "pick_num_splits",
+    "decode_partials", "split_reduce",
+]

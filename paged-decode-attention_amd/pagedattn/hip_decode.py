@@ -1,0 +1,325 @@
+"""Host wrapper of the gfx950 paged decode kernels.
+
+Same call surface as the reference's `paged_decode_triton`
+(ParamThakkar123/paged-decode-attention, pagedattn/triton_decode.py:285-377)
+and `pick_num_splits` (:248-263); the launch itself goes through the C ABI of
+`libpagedattn_hip.so` (include/pagedattn.h). Nothing here computes attention:
+if the library is missing or the tensors are not on a GPU, the call raises.
+
+Knobs of the reference that only steer Triton code generation (`per_page_bt`,
+`num_warps`, `num_stages`) are accepted and ignored: the HIP kernel always
+reads one block-table entry per 16-token sub-tile (one per page at page size
+16) and has a fixed 4-wave workgroup. `block_n` keeps the reference's check
+that it is a multiple of the page size; split ranges are aligned to the
+kernel's 32-token tile.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+
+import torch
+
+from . import _abi
+from .cache import PagedKVCache
+
+# Work geometry of the decode kernel (csrc/paged_decode.hip): 4 wave64s per
+# workgroup, 32 tokens per wave iteration.
+WAVES_PER_WORKGROUP = 4
+TILE_TOKENS = 32
+# Workgroups of the decode kernel that fit on one CU at once at head_dim 128
+# (two 4-wave workgroups: 225 VGPR+AGPR per lane -> 2 waves per SIMD).
+RESIDENT_WORKGROUPS_PER_CU = 2
+
+_KV_CODE = {"fp16": _abi.PA_KV_FP16, "fp8_e5m2": _abi.PA_KV_FP8_E5M2, "int8": _abi.PA_KV_INT8}
+_STORE_DTYPE = {"fp16": torch.float16, "fp8_e5m2": torch.float8_e5m2, "int8": torch.int8}
+_SCALE_CODE = {torch.float16: _abi.PA_SCALE_FP16, torch.float32: _abi.PA_SCALE_FP32}
+
+
+def pick_num_splits(
+    batch: int, num_kv_heads: int, max_seq_len: int, sm_count: int, block_n: int = 64
+) -> int:
+    """Split count for the split-KV path, sized for the MI355X's 256 CUs.
+
+    Same signature as the reference (triton_decode.py:248-263), MI355X policy:
+    launch enough (batch, kv_head, split) workgroups to occupy every CU with
+    RESIDENT_WORKGROUPS_PER_CU workgroups, but never give a wave fewer than two
+    32-token tiles. No power-of-two rounding and no cap of 64, so a
+    long-context batch of 4 can use hundreds of splits. `block_n` is accepted
+    for signature compatibility.
+    """
+    del block_n
+    base = max(1, batch * num_kv_heads)
+    target = RESIDENT_WORKGROUPS_PER_CU * max(1, sm_count)
+    if base >= target:
+        return 1
+    want = -(-target // base)
+    max_useful = max(1, max_seq_len // (2 * WAVES_PER_WORKGROUP * TILE_TOKENS))
+    return int(max(1, min(want, max_useful, _abi.PA_MAX_SPLITS)))
+
+
+class _Workspace:
+    """Split-KV scratch (fp32 partial outputs and log2-sum-exps), per device.
+
+    Grows to the largest request seen and hands out views, so repeated calls
+    allocate nothing (the role of the reference's `_WS`, triton_decode.py:266-282).
+    """
+
+    def __init__(self) -> None:
+        self._buf: dict[torch.device, tuple[torch.Tensor, torch.Tensor]] = {}
+        self._lock = threading.Lock()
+
+    def get(self, b: int, hq: int, splits: int, d: int, device) -> tuple[torch.Tensor, torch.Tensor]:
+        n_out = b * hq * splits * d
+        n_lse = b * hq * splits
+        with self._lock:
+            cur = self._buf.get(device)
+            if cur is None or cur[0].numel() < n_out or cur[1].numel() < n_lse:
+                cur = (
+                    torch.empty(max(n_out, 1), dtype=torch.float32, device=device),
+                    torch.empty(max(n_lse, 1), dtype=torch.float32, device=device),
+                )
+                self._buf[device] = cur
+        return cur[0][:n_out].view(b, hq, splits, d), cur[1][:n_lse].view(b, hq, splits)
+
+
+_WS = _Workspace()
+_CU_COUNT: dict[int, int] = {}
+
+
+def _cu_count(device: torch.device) -> int:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    n = _CU_COUNT.get(idx)
+    if n is None:
+        n = torch.cuda.get_device_properties(idx).multi_processor_count
+        _CU_COUNT[idx] = n
+    return n
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _fill_args(
+    q: torch.Tensor,
+    cache: PagedKVCache,
+    out: torch.Tensor,
+    num_splits: int,
+    sm_scale: float,
+    part_out: torch.Tensor | None,
+    part_lse: torch.Tensor | None,
+) -> _abi.PaDecodeArgs:
+    b, hq, d = q.shape
+    shape = cache.shape
+    if cache.kv_dtype not in _KV_CODE:
+        raise NotImplementedError(f"kv_dtype {cache.kv_dtype!r} is not supported by the HIP kernel")
+    if q.dtype != torch.float16 or out.dtype != torch.float16:
+        raise NotImplementedError(f"q/out dtype {q.dtype}/{out.dtype}: only float16 is supported")
+    if q.device.type != "cuda":
+        raise ValueError(f"q is on {q.device}: the HIP decode kernel needs GPU tensors")
+    k, v = cache.k_cache, cache.v_cache
+    for name, t in (("k_cache", k), ("v_cache", v), ("out", out),
+                    ("block_table", cache.block_table), ("seq_lens", cache.seq_lens)):
+        if t.device != q.device:
+            raise ValueError(f"{name} is on {t.device}, q on {q.device}")
+    if k.dtype != _STORE_DTYPE[cache.kv_dtype] or v.dtype != k.dtype:
+        raise ValueError(f"k/v cache dtype {k.dtype}/{v.dtype} does not match kv_dtype {cache.kv_dtype}")
+    if k.dim() != 4 or tuple(k.shape[1:]) != (cache.block_size, shape.num_kv_heads, d):
+        raise ValueError(f"k_cache shape {tuple(k.shape)} is not [NB, {cache.block_size}, "
+                         f"{shape.num_kv_heads}, {d}]")
+    if tuple(v.shape) != tuple(k.shape) or v.stride() != k.stride():
+        raise ValueError("v_cache must have k_cache's shape and strides")
+    if k.stride(3) != 1 or q.stride(2) != 1 or out.stride(2) != 1:
+        raise ValueError("head_dim must be the contiguous (stride-1) dimension of q, out and the caches")
+    if tuple(out.shape) != (b, hq, d):
+        raise ValueError(f"out shape {tuple(out.shape)} != {(b, hq, d)}")
+    bt, sl = cache.block_table, cache.seq_lens
+    if bt.dtype != torch.int32 or sl.dtype != torch.int32:
+        raise ValueError("block_table and seq_lens must be int32")
+    if bt.dim() != 2 or bt.shape[0] != b or sl.shape != (b,):
+        raise ValueError(f"block_table {tuple(bt.shape)} / seq_lens {tuple(sl.shape)} do not match batch {b}")
+    if bt.stride(1) != 1 or sl.stride(0) != 1:
+        raise ValueError("block_table rows and seq_lens must be contiguous")
+
+    a = _abi.PaDecodeArgs()
+    a.q = q.data_ptr()
+    a.k_cache = k.data_ptr()
+    a.v_cache = v.data_ptr()
+    a.out = out.data_ptr()
+    a.block_table = bt.data_ptr()
+    a.seq_lens = sl.data_ptr()
+    a.batch = b
+    a.num_q_heads = hq
+    a.num_kv_heads = shape.num_kv_heads
+    a.head_dim = d
+    a.block_size = cache.block_size
+    a.num_blocks = k.shape[0]
+    a.max_blocks = bt.shape[1]
+    a.num_splits = num_splits
+    a.stride_qb, a.stride_qh = q.stride(0), q.stride(1)
+    a.stride_kn, a.stride_kt, a.stride_kh = k.stride(0), k.stride(1), k.stride(2)
+    a.stride_ob, a.stride_oh = out.stride(0), out.stride(1)
+    a.stride_btb = bt.stride(0)
+    a.kv_dtype = _KV_CODE[cache.kv_dtype]
+    a.io_dtype = _abi.PA_IO_FP16
+    a.sm_scale = sm_scale
+    if cache.kv_dtype == "int8":
+        ks, vs = cache.k_scale, cache.v_scale
+        if ks is None or vs is None:
+            raise ValueError("int8 cache needs k_scale and v_scale")
+        if ks.dtype not in _SCALE_CODE or vs.dtype != ks.dtype:
+            raise ValueError(f"int8 scales must be float16 or float32, got {ks.dtype}/{vs.dtype}")
+        if tuple(ks.shape) != tuple(k.shape[:3]) or vs.stride() != ks.stride() or ks.stride(2) != 1:
+            raise ValueError("k_scale/v_scale must be [NB, block_size, H_kv] with equal strides "
+                             "and a contiguous head dimension")
+        if ks.device != q.device or vs.device != q.device:
+            raise ValueError("scales must live on q's device")
+        a.k_scale = ks.data_ptr()
+        a.v_scale = vs.data_ptr()
+        a.stride_sn, a.stride_st = ks.stride(0), ks.stride(1)
+        a.scale_dtype = _SCALE_CODE[ks.dtype]
+    else:
+        a.scale_dtype = _abi.PA_SCALE_NONE
+    if part_out is not None:
+        a.part_out = part_out.data_ptr()
+        a.part_lse = part_lse.data_ptr()
+        a.stride_pb, a.stride_ph, a.stride_ps = part_out.stride(0), part_out.stride(1), part_out.stride(2)
+        a.stride_lb, a.stride_lh = part_lse.stride(0), part_lse.stride(1)
+    return a
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def paged_decode_hip(
+    q: torch.Tensor,
+    cache: PagedKVCache,
+    out: torch.Tensor | None = None,
+    block_n: int = 64,
+    num_splits: int | None = None,
+    per_page_bt: bool = True,
+    num_warps: int = 4,
+    num_stages: int = 3,
+    sm_scale: float | None = None,
+) -> torch.Tensor:
+    """Paged GQA decode attention. q: [B, Hq, D] fp16 -> [B, Hq, D] fp16.
+
+    Reference: pagedattn/triton_decode.py:285-377. `sm_scale` overrides the
+    default 1/sqrt(head_dim) (a serving runtime may fold other factors in).
+    With `num_splits=None` the split count comes from `pick_num_splits`, which
+    needs `seq_lens.max()` on the host (a device sync, as in the reference);
+    serving callers pass `num_splits` to avoid it. A sequence with
+    seq_len == 0 produces zeros.
+    """
+    del per_page_bt, num_warps, num_stages
+    b, hq, d = q.shape
+    shape = cache.shape
+    hkv = shape.num_kv_heads
+    group = shape.gqa_group
+    assert d == shape.head_dim
+    assert block_n % cache.block_size == 0, "BLOCK_N must be a multiple of the page size"
+    if hq != hkv * group:
+        raise ValueError(f"q has {hq} heads, cache shape expects {hkv * group}")
+
+    if out is None:
+        out = torch.empty((b, hq, d), dtype=q.dtype, device=q.device)
+    if b == 0:
+        return out
+    if num_splits is None:
+        max_seq = int(cache.seq_lens.max().item())
+        num_splits = pick_num_splits(b, hkv, max_seq, _cu_count(q.device), block_n)
+    num_splits = int(num_splits)
+    scale = shape.softmax_scale if sm_scale is None else float(sm_scale)
+
+    part_out = part_lse = None
+    if num_splits > 1:
+        part_out, part_lse = _WS.get(b, hq, num_splits, d, q.device)
+    args = _fill_args(q, cache, out, num_splits, scale, part_out, part_lse)
+    lib = _abi.load()
+    with torch.cuda.device(q.device):
+        rc = lib.pa_decode(ctypes.byref(args), _stream(q.device))
+    _abi.check(rc, "pa_decode")
+    return out
+
+
+# Import-path compatibility with the reference (pagedattn.triton_decode.
+# paged_decode_triton): the same function, HIP underneath.
+paged_decode_triton = paged_decode_hip
+
+
+def decode_partials(
+    q: torch.Tensor,
+    cache: PagedKVCache,
+    num_splits: int,
+    sm_scale: float | None = None,
+    part_out: torch.Tensor | None = None,
+    part_lse: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Run only the decode pass; returns (part_out [B,Hq,S,D], part_lse [B,Hq,S]).
+
+    part_lse is log2(sum_j 2^(s_j)) of the split's scaled logits s = q.k *
+    sm_scale * log2(e) and part_out the split's normalised output, the format
+    of the reference's split epilogue (triton_decode.py:169-188).
+    """
+    b, hq, d = q.shape
+    scale = cache.shape.softmax_scale if sm_scale is None else float(sm_scale)
+    if part_out is None:
+        part_out = torch.empty((b, hq, num_splits, d), dtype=torch.float32, device=q.device)
+    if part_lse is None:
+        part_lse = torch.empty((b, hq, num_splits), dtype=torch.float32, device=q.device)
+    out = torch.empty((b, hq, d), dtype=q.dtype, device=q.device)
+    args = _fill_args(q, cache, out, num_splits, scale, part_out, part_lse)
+    lib = _abi.load()
+    with torch.cuda.device(q.device):
+        rc = lib.pa_decode_partials(ctypes.byref(args), _stream(q.device))
+    _abi.check(rc, "pa_decode_partials")
+    return part_out, part_lse
+
+
+def split_reduce(
+    part_out: torch.Tensor, part_lse: torch.Tensor, out: torch.Tensor | None = None
+) -> torch.Tensor:
+    """Merge split partials into [B, H, D] fp16 (triton_decode.py:198-240)."""
+    b, h, s, d = part_out.shape
+    if part_out.dtype != torch.float32 or part_lse.dtype != torch.float32:
+        raise ValueError("partials must be float32")
+    if part_out.stride(3) != 1 or tuple(part_lse.shape) != (b, h, s):
+        raise ValueError("part_out must have a contiguous head dim and part_lse shape [B, H, S]")
+    if out is None:
+        out = torch.empty((b, h, d), dtype=torch.float16, device=part_out.device)
+    if out.dtype != torch.float16 or out.stride(2) != 1:
+        raise ValueError("out must be float16 with a contiguous head dim")
+    r = _abi.PaReduceArgs()
+    r.part_out = part_out.data_ptr()
+    r.part_lse = part_lse.data_ptr()
+    r.out = out.data_ptr()
+    r.batch, r.num_heads, r.head_dim, r.num_splits = b, h, d, s
+    r.stride_pb, r.stride_ph, r.stride_ps = part_out.stride(0), part_out.stride(1), part_out.stride(2)
+    r.stride_lb, r.stride_lh = part_lse.stride(0), part_lse.stride(1)
+    r.stride_ob, r.stride_oh = out.stride(0), out.stride(1)
+    r.io_dtype = _abi.PA_IO_FP16
+    lib = _abi.load()
+    with torch.cuda.device(part_out.device):
+        rc = lib.pa_split_reduce(ctypes.byref(r), _stream(part_out.device))
+    _abi.check(rc, "pa_split_reduce")
+    return out
+
+
+def split_count_for(cache: PagedKVCache, device: torch.device) -> int:
+    """The split count `paged_decode_hip(num_splits=None)` would choose."""
+    max_seq = int(cache.seq_lens.max().item()) if cache.batch else 0
+    return pick_num_splits(cache.batch, cache.shape.num_kv_heads, max_seq, _cu_count(device))
+
+
+__all__ = [
+    "paged_decode_hip",
+    "paged_decode_triton",
+    "pick_num_splits",
+    "decode_partials",
+    "split_reduce",
+    "split_count_for",
+    "WAVES_PER_WORKGROUP",
+    "TILE_TOKENS",
+]
