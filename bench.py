@@ -1,0 +1,362 @@
+"""Benchmark of the MI355X paged GQA decode path (one GPU).
+
+Workload (the headline "Llama-3-8B shape"): batch 64,
+32 q / 8 kv heads, head_dim 128, page 16, every sequence 4096 tokens, fp16
+paged KV in a fully permuted 16,384-block pool, split-KV on. One "step" is one
+decode call (`pagedattn.paged_decode_triton`) over the whole batch, inputs
+resident in HBM. K/V are rotated over `--copies` identical pool copies so the
+256 MB MALL cannot serve a call from the previous one.
+
+Prints ONE JSON line: value = algorithmic HBM GB/s of a whole decode call
+(K+V+q+out+block-table bytes / call time), plus µs/call, a roofline object for
+the dominant decode kernel (HIP-event timed, launched alone) and a CPU
+baseline (the torch fp32 oracle on a bounded sample of the same workload).
+
+    python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--config c2]
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import dataclasses
+import json
+import math
+import os
+import pathlib
+import sys
+import time
+import types
+
+ROOT = pathlib.Path(__file__).resolve().parent
+PKG = ROOT / "paged-decode-attention_amd"
+for _p in (str(PKG), str(ROOT)):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
+
+
+def _log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+@dataclasses.dataclass
+class Workload:
+    name: str
+    shape_name: str
+    batch: int
+    lens: list
+    kv_dtype: str
+    scale_fp32: bool
+    pool_blocks: int
+    seed: int
+    description: str
+
+
+def make_workload(cfg: str) -> Workload:
+    """The BASELINE.json configs, generated deterministically."""
+    import torch
+
+    from pagedattn import LLAMA3_8B, LLAMA3_70B, QWEN25_05B
+
+    if cfg == "c1":
+        g = torch.Generator().manual_seed(0)
+        lens = torch.randint(32, 193, (24,), generator=g).tolist()
+        return Workload("c1", QWEN25_05B.name, 24, lens, "fp16", False, 512, 0,
+                        "Qwen2.5-0.5B shape 14q/2kv d64, B=24, T~U[32,192], fp16, 512-block pool")
+    if cfg == "c2":
+        return Workload("c2", LLAMA3_8B.name, 64, [4096] * 64, "fp16", False, 64 * 256, 1,
+                        "Llama-3-8B shape 32q/8kv d128, B=64, T=4096, fp16, page 16")
+    if cfg == "c3":
+        g = torch.Generator().manual_seed(2)
+        u = torch.rand(64, generator=g, dtype=torch.float64)
+        lens = torch.exp(math.log(128) + u * (math.log(8192) - math.log(128))).round().long().tolist()
+        nb = sum(-(-t // 16) for t in lens)
+        return Workload("c3", LLAMA3_8B.name, 64, lens, "fp8_e5m2", False, nb, 2,
+                        "Llama-3-8B shape, fp8_e5m2 KV, B=64, T log-uniform 128..8192")
+    if cfg == "c4":
+        return Workload("c4", LLAMA3_70B.name, 32, [16384] * 32, "int8", True, 32 * 1024, 3,
+                        "64q/8kv d128 (g8), B=32, T=16384, int8 KV + fp32 per-(token,head) scales")
+    if cfg == "c5":
+        return Workload("c5", LLAMA3_8B.name, 4, [131072] * 4, "fp16", False, 40_000, 4,
+                        "32q/8kv d128, B=4, T=131072, fp16, 40k-block shuffled pool")
+    raise SystemExit(f"unknown config {cfg}")
+
+
+def shape_of(name: str):
+    from pagedattn import LLAMA3_8B, LLAMA3_70B, QWEN25_05B
+
+    return {s.name: s for s in (LLAMA3_8B, LLAMA3_70B, QWEN25_05B)}[name]
+
+
+def subset_cache(cache, rows):
+    """CPU copy of batch rows `rows` of a device cache, blocks renumbered."""
+    import torch
+
+    bt = cache.block_table.cpu()
+    lens = cache.seq_lens.cpu()
+    bs = cache.block_size
+    ids, new_bt = [], []
+    for r in rows:
+        n = -(-int(lens[r]) // bs)
+        base = sum(len(x) for x in ids)
+        ids.append(bt[r, :n].long())
+        row = torch.zeros(bt.shape[1], dtype=torch.int32)
+        row[:n] = torch.arange(base, base + n, dtype=torch.int32)
+        new_bt.append(row)
+    dev_ids = torch.cat(ids).to(cache.k_cache.device)
+    pick = lambda t: None if t is None else t.index_select(0, dev_ids).cpu()
+    return types.SimpleNamespace(
+        shape=cache.shape, block_size=bs, kv_dtype=cache.kv_dtype,
+        k_cache=pick(cache.k_cache), v_cache=pick(cache.v_cache),
+        k_scale=pick(cache.k_scale), v_scale=pick(cache.v_scale),
+        block_table=torch.stack(new_bt), seq_lens=lens[list(rows)].clone(),
+    )
+
+
+def cpu_baseline(q, cache, budget_s: float) -> dict:
+    """The torch fp32 oracle (a port of pagedattn/reference.py:28-49) timed on
+    the host on a bounded sample of the workload's sequences."""
+    import torch
+
+    from oracle import reference as oracle
+
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    b = cache.batch
+    probe = subset_cache(cache, [0])
+    t0 = time.perf_counter()
+    oracle.reference_decode(q[:1].cpu(), probe)
+    per_seq = max(time.perf_counter() - t0, 1e-4)
+    runs = 3
+    n = int(max(1, min(b, budget_s / (runs * per_seq))))
+    rows = list(range(n))
+    sub = subset_cache(cache, rows)
+    qs = q[:n].cpu()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        oracle.reference_decode(qs, sub)
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[len(times) // 2]
+    sub_bytes = _algorithmic_bytes(sub)
+    return {
+        "value": round(sub_bytes / med / 1e9, 4),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"oracle.reference_decode (torch fp32 CPU, gather+per-head einsum) on the first "
+                  f"{n} of {b} sequences, median of {runs} runs: {med * 1e3:.1f} ms for "
+                  f"{sub_bytes / 1e6:.1f} MB algorithmic; full-call equivalent "
+                  f"{med * b / n * 1e3:.0f} ms",
+    }
+
+
+def _algorithmic_bytes(cache) -> int:
+    """K/V (+ int8 scales) inside the sequences + q + out (fp16) + used
+    block-table entries."""
+    import torch
+
+    lens = cache.seq_lens.cpu().long()
+    s = cache.shape
+    n_tok = int(lens.sum())
+    elem = cache.k_cache.element_size()
+    kv = 2 * n_tok * s.num_kv_heads * s.head_dim * elem
+    if cache.kv_dtype == "int8":
+        kv += 2 * n_tok * s.num_kv_heads * cache.k_scale.element_size()
+    pages = int(((lens + cache.block_size - 1) // cache.block_size).sum())
+    b = int(lens.numel())
+    return kv + 2 * b * s.num_q_heads * s.head_dim * 2 + 4 * pages
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--splits", type=int, default=None, help="override the split count")
+    ap.add_argument("--copies", type=int, default=None, help="pool copies rotated between calls")
+    ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run a 1 GiB device copy (PMC calibration of FETCH/WRITE_SIZE)")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the decode shards over (batch, kv_head) with no exchange; see the "
+              "sharding notes in DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from pagedattn import allocate, pick_num_splits
+    from pagedattn.hip_decode import _WS, _cu_count, decode_partials, paged_decode_hip
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    wl = make_workload(args.config)
+    shape = shape_of(wl.shape_name)
+    used = sum(-(-t // 16) for t in wl.lens)
+    _log(f"config {wl.name}: {wl.description}; pool {wl.pool_blocks} blocks ({used} used)")
+    t0 = time.perf_counter()
+    cache = allocate(shape, wl.batch, wl.lens, block_size=16, kv_dtype=wl.kv_dtype, device="cuda",
+                     seed=wl.seed, slack_blocks=wl.pool_blocks - used,
+                     scale_dtype=torch.float32 if wl.scale_fp32 else torch.float16,
+                     fill_device="cuda")
+    g = torch.Generator().manual_seed(100 + wl.seed)
+    q = torch.randn((wl.batch, shape.num_q_heads, shape.head_dim), dtype=torch.float16,
+                    generator=g).to(dev)
+    pool_bytes = 2 * cache.k_cache.numel() * cache.k_cache.element_size()
+    copies = args.copies or max(1, math.ceil(512e6 / pool_bytes) + 1)
+    caches = [cache]
+    for _ in range(copies - 1):
+        caches.append(dataclasses.replace(
+            cache, k_cache=cache.k_cache.clone(), v_cache=cache.v_cache.clone(),
+            k_scale=None if cache.k_scale is None else cache.k_scale.clone(),
+            v_scale=None if cache.v_scale is None else cache.v_scale.clone()))
+    torch.cuda.synchronize()
+    _log(f"allocated {copies} pool copies of {pool_bytes / 2**30:.2f} GiB in {time.perf_counter() - t0:.1f} s")
+
+    cus = _cu_count(dev)
+    splits = args.splits or pick_num_splits(wl.batch, shape.num_kv_heads, max(wl.lens), cus)
+    out = torch.empty_like(q)
+    algo = _algorithmic_bytes(cache)
+    kv_only = cache.bytes_read_per_decode_step()
+    _log(f"{cus} CUs, num_splits={splits}, algorithmic bytes/call={algo}")
+
+    # parity on a sample of sequences against the CPU oracle, and bit stability
+    from oracle import reference as oracle
+
+    paged_decode_hip(q, cache, out=out, num_splits=splits)
+    first = out.clone()
+    paged_decode_hip(q, cache, out=out, num_splits=splits)
+    torch.cuda.synchronize()
+    bit_stable = bool(torch.equal(first, out))
+    rows = sorted({0, wl.batch // 2, wl.batch - 1})
+    ref = oracle.reference_decode(q[rows].cpu(), subset_cache(cache, rows), out_dtype=torch.float32)
+    max_abs = (out[rows].float().cpu() - ref).abs().max().item()
+    _log(f"parity on rows {rows}: max_abs_err={max_abs:.3e}; bit_stable={bit_stable}")
+    if not (max_abs < 2e-3) or not bit_stable:
+        _log("PARITY FAILURE")
+        return 1
+
+    if args.calib_copy:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    # whole-call timing (decode + reduce when split), rotating pool copies
+    for i in range(args.warmup):
+        paged_decode_hip(q, caches[i % copies], out=out, num_splits=splits)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    t_wall = time.perf_counter()
+    for i in range(args.steps):
+        paged_decode_hip(q, caches[i % copies], out=out, num_splits=splits)
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    ms_step = ev0.elapsed_time(ev1) / args.steps
+    _log(f"whole call: {ms_step * 1e3:.1f} us/call (wall {wall / args.steps * 1e6:.1f} us/call)")
+
+    # the dominant kernel alone: the decode pass (partials when split)
+    if splits > 1:
+        part_out, part_lse = _WS.get(wl.batch, shape.num_q_heads, splits, shape.head_dim, dev)
+        run = lambda c: decode_partials(q, c, splits, part_out=part_out, part_lse=part_lse)
+    else:
+        run = lambda c: paged_decode_hip(q, c, out=out, num_splits=1)
+    for i in range(args.warmup):
+        run(caches[i % copies])
+    torch.cuda.synchronize()
+    ev0.record()
+    for i in range(args.steps):
+        run(caches[i % copies])
+    ev1.record()
+    torch.cuda.synchronize()
+    kern_us = ev0.elapsed_time(ev1) / args.steps * 1e3
+    _log(f"decode kernel alone: {kern_us:.1f} us/launch")
+
+    reduce_us = None
+    if splits > 1:
+        from pagedattn.hip_decode import split_reduce
+
+        for _ in range(args.warmup):
+            split_reduce(part_out, part_lse, out)
+        ev0.record()
+        for _ in range(args.steps):
+            split_reduce(part_out, part_lse, out)
+        ev1.record()
+        torch.cuda.synchronize()
+        reduce_us = ev0.elapsed_time(ev1) / args.steps * 1e3
+        _log(f"split reduce alone: {reduce_us:.2f} us/launch")
+
+    traffic = None
+    tfile = ROOT / "profiles" / "traffic.json"
+    if tfile.exists():
+        try:
+            traffic = json.loads(tfile.read_text()).get(wl.name, {}).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+
+    achieved_kernel = algo / (kern_us * 1e-6) / 1e9
+    value = algo / (ms_step * 1e-3) / 1e9
+    result = {
+        "metric": "decode attn µs/call + achieved HBM GB/s (% of peak), Llama-3-8B shape",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "us_per_call": round(ms_step * 1e3, 2),
+        "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {"fp16": "fp16", "fp8_e5m2": "fp8_e5m2", "int8": "int8"}[wl.kv_dtype],
+        "data": "synthetic (seeded N(0,1) fp16 K/V/q, permuted block pool)",
+        "config": {
+            "workload": f"{wl.name}: {wl.description}",
+            "batch": wl.batch,
+            "num_q_heads": shape.num_q_heads,
+            "num_kv_heads": shape.num_kv_heads,
+            "head_dim": shape.head_dim,
+            "block_size": 16,
+            "seq_len_max": max(wl.lens),
+            "num_splits": splits,
+            "pool_copies_rotated": copies,
+            "parallelism": "single GPU",
+        },
+        "algorithmic_bytes_per_call": algo,
+        "kv_bytes_per_call": kv_only,
+        "parity_max_abs_err": max_abs,
+        "bit_stable": bit_stable,
+        "split_reduce_us": None if reduce_us is None else round(reduce_us, 3),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved_kernel, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved_kernel / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "kernel": "paged_decode_kernel",
+            "kernel_us": round(kern_us, 2),
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(q, cache, args.cpu_budget)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,247 @@
+"""CPU tests of the host side: the C ABI surface, argument validation, the
+Python mirror of the reference interface, split policy, cache generation and
+byte accounting. Nothing here launches a kernel."""
+
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import re
+import subprocess
+import types
+
+import pytest
+import torch
+
+from pagedattn import (LLAMA3_8B, LLAMA3_70B, MHA_DEBUG, QWEN25_05B, ModelShape, allocate,
+                       kv_bytes_per_token, pick_num_splits)
+from pagedattn import _abi
+from pagedattn.hip_decode import paged_decode_hip
+
+ROOT = pathlib.Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "pagedattn.h"
+
+
+def _lib():
+    if not _abi.lib_path().exists():
+        import __graft_entry__
+
+        __graft_entry__.build()
+    return _abi.load()
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pa_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_bound_symbols():
+    assert _declared_functions() == sorted(_abi.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib()
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+    nm = subprocess.run(["nm", "-D", "--defined-only", str(_abi.lib_path())],
+                        capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (pa_\w+)", nm))
+    assert exported == set(_declared_functions())
+    assert lib.pa_abi_version() == _abi.PA_ABI_VERSION
+
+
+def test_struct_layout_matches_header(tmp_path):
+    """ctypes mirrors of pa_decode_args / pa_reduce_args against gcc's layout."""
+    lines = ['#include <stddef.h>', '#include <stdio.h>', '#include "pagedattn.h"', 'int main(void){']
+    for cname, cls in (("pa_decode_args", _abi.PaDecodeArgs), ("pa_reduce_args", _abi.PaReduceArgs)):
+        lines.append(f'printf("{cname} sizeof %zu\\n", sizeof({cname}));')
+        for f, _ in cls._fields_:
+            lines.append(f'printf("{cname} {f} %zu\\n", offsetof({cname}, {f}));')
+    lines.append("return 0;}")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)], check=True)
+    got = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")
+    table = {}
+    for line in filter(None, got):
+        s, f, v = line.split()
+        table[(s, f)] = int(v)
+    for cname, cls in (("pa_decode_args", _abi.PaDecodeArgs), ("pa_reduce_args", _abi.PaReduceArgs)):
+        assert table[(cname, "sizeof")] == ctypes.sizeof(cls)
+        for f, _ in cls._fields_:
+            assert table[(cname, f)] == getattr(cls, f).offset, (cname, f)
+
+
+def test_constants_match_header():
+    text = HEADER.read_text()
+    for name in ("PA_ABI_VERSION", "PA_OK", "PA_ERR_INVALID", "PA_ERR_UNSUPPORTED", "PA_ERR_HIP",
+                 "PA_KV_FP16", "PA_KV_FP8_E5M2", "PA_KV_INT8", "PA_SCALE_NONE", "PA_SCALE_FP16",
+                 "PA_SCALE_FP32", "PA_IO_FP16", "PA_MAX_SPLITS", "PA_MAX_GROUP"):
+        m = re.search(rf"#define {name} \(?(-?\d+)\)?", text)
+        assert m, name
+        assert int(m.group(1)) == getattr(_abi, name), name
+
+
+# --------------------------------------------------------------------------
+# argument validation through the C ABI: every case is rejected before any
+# HIP call, so fake device addresses are never dereferenced. Skipped where a
+# GPU is visible, so no such call can ever reach a device.
+# --------------------------------------------------------------------------
+
+cpu_only = pytest.mark.skipif(torch.cuda.is_available(), reason="fake-pointer validation runs on CPU hosts only")
+
+FAKE = 0x10000  # 16-byte aligned, never dereferenced
+
+
+def _valid_args(**over):
+    a = _abi.PaDecodeArgs()
+    a.q = a.k_cache = a.v_cache = a.out = a.block_table = a.seq_lens = FAKE
+    a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim = 2, 32, 8, 128
+    a.block_size, a.num_blocks, a.max_blocks, a.num_splits = 16, 64, 8, 1
+    a.stride_qb, a.stride_qh = 32 * 128, 128
+    a.stride_kn, a.stride_kt, a.stride_kh = 16 * 8 * 128, 8 * 128, 128
+    a.stride_ob, a.stride_oh = 32 * 128, 128
+    a.stride_btb = 8
+    a.kv_dtype, a.scale_dtype, a.io_dtype = _abi.PA_KV_FP16, _abi.PA_SCALE_NONE, _abi.PA_IO_FP16
+    a.sm_scale = 128 ** -0.5
+    for k, v in over.items():
+        setattr(a, k, v)
+    return a
+
+
+INVALID = [
+    ("q", dict(q=None), _abi.PA_ERR_INVALID),
+    ("batch", dict(batch=-1), _abi.PA_ERR_INVALID),
+    ("heads", dict(num_q_heads=30), _abi.PA_ERR_INVALID),
+    ("kv_heads", dict(num_kv_heads=0), _abi.PA_ERR_INVALID),
+    ("head_dim", dict(head_dim=96), _abi.PA_ERR_UNSUPPORTED),
+    ("page", dict(block_size=24), _abi.PA_ERR_UNSUPPORTED),
+    ("page8", dict(block_size=8), _abi.PA_ERR_UNSUPPORTED),
+    ("splits0", dict(num_splits=0), _abi.PA_ERR_INVALID),
+    ("splits_big", dict(num_splits=_abi.PA_MAX_SPLITS + 1), _abi.PA_ERR_INVALID),
+    ("no_workspace", dict(num_splits=4), _abi.PA_ERR_INVALID),
+    ("kv_dtype", dict(kv_dtype=7), _abi.PA_ERR_INVALID),
+    ("io_dtype", dict(io_dtype=3), _abi.PA_ERR_UNSUPPORTED),
+    ("int8_no_scale", dict(kv_dtype=_abi.PA_KV_INT8, scale_dtype=_abi.PA_SCALE_FP16), _abi.PA_ERR_INVALID),
+    ("int8_scale_type", dict(kv_dtype=_abi.PA_KV_INT8, k_scale=FAKE, v_scale=FAKE), _abi.PA_ERR_INVALID),
+    ("scale_on_fp16", dict(scale_dtype=_abi.PA_SCALE_FP32), _abi.PA_ERR_INVALID),
+    ("misaligned_q", dict(q=FAKE + 2), _abi.PA_ERR_INVALID),
+    ("misaligned_head_stride", dict(stride_kh=100), _abi.PA_ERR_INVALID),
+    ("negative_stride", dict(stride_kt=-1024), _abi.PA_ERR_INVALID),
+    ("no_blocks", dict(num_blocks=0), _abi.PA_ERR_INVALID),
+    ("misaligned_workspace", dict(num_splits=2, part_out=FAKE + 4, part_lse=FAKE,
+                                  stride_pb=1, stride_ph=1, stride_ps=128), _abi.PA_ERR_INVALID),
+]
+
+
+@cpu_only
+@pytest.mark.parametrize("name,over,code", INVALID, ids=[c[0] for c in INVALID])
+def test_pa_decode_rejects(name, over, code):
+    lib = _lib()
+    a = _valid_args(**over)
+    assert lib.pa_decode(ctypes.byref(a), None) == code
+    msg = lib.pa_last_error().decode()
+    assert msg, "no error message recorded"
+    assert lib.pa_decode_partials(ctypes.byref(a), None) < 0
+
+
+@cpu_only
+def test_null_args_and_reduce_validation():
+    lib = _lib()
+    assert lib.pa_decode(None, None) == _abi.PA_ERR_INVALID
+    assert lib.pa_split_reduce(None, None) == _abi.PA_ERR_INVALID
+    r = _abi.PaReduceArgs()
+    r.part_out = r.part_lse = r.out = FAKE
+    r.batch, r.num_heads, r.head_dim, r.num_splits = 1, 4, 100, 2
+    assert lib.pa_split_reduce(ctypes.byref(r), None) == _abi.PA_ERR_UNSUPPORTED
+    r.head_dim, r.num_splits = 128, 0
+    assert lib.pa_split_reduce(ctypes.byref(r), None) == _abi.PA_ERR_INVALID
+    r.num_splits, r.stride_ob = 2, -1
+    assert lib.pa_split_reduce(ctypes.byref(r), None) == _abi.PA_ERR_INVALID
+
+
+def test_python_errors_from_codes():
+    with pytest.raises(ValueError):
+        _abi.check(_abi.PA_ERR_INVALID, "x")
+    with pytest.raises(NotImplementedError):
+        _abi.check(_abi.PA_ERR_UNSUPPORTED, "x")
+    with pytest.raises(RuntimeError):
+        _abi.check(_abi.PA_ERR_HIP, "x")
+    _abi.check(_abi.PA_OK, "x")
+
+
+# --------------------------------------------------------------------------
+# the Python mirror of the reference interface
+# --------------------------------------------------------------------------
+
+def test_no_cpu_fallback():
+    c = allocate(LLAMA3_8B, 2, [10, 20], device="cpu", seed=0)
+    q = torch.randn((2, 32, 128), dtype=torch.float16)
+    with pytest.raises(ValueError, match="GPU"):
+        paged_decode_hip(q, c, num_splits=1)
+
+
+def test_reference_names_resolve_to_hip():
+    import pagedattn
+    from pagedattn import triton_decode
+
+    assert pagedattn.paged_decode_triton is paged_decode_hip
+    assert triton_decode.paged_decode_triton is paged_decode_hip
+    assert triton_decode.pick_num_splits is pick_num_splits
+
+
+def test_model_shapes():
+    assert LLAMA3_8B.gqa_group == 4 and LLAMA3_70B.gqa_group == 8
+    assert MHA_DEBUG.gqa_group == 1 and QWEN25_05B.gqa_group == 7
+    assert LLAMA3_8B.softmax_scale == 128 ** -0.5
+    with pytest.raises(AssertionError):
+        ModelShape(30, 8, 128).gqa_group
+
+
+def test_kv_bytes_per_token():
+    assert kv_bytes_per_token(LLAMA3_8B, "fp16") == 2 * 8 * 128 * 2
+    assert kv_bytes_per_token(LLAMA3_8B, "fp8_e5m2") == 2 * 8 * 128
+    assert kv_bytes_per_token(LLAMA3_8B, "int8") == 2 * 8 * 128 + 2 * 8 * 2
+    assert kv_bytes_per_token(LLAMA3_8B, "int8", torch.float32) == 2 * 8 * 128 + 2 * 8 * 4
+
+
+def test_pick_num_splits_policy():
+    # enough work already: no split
+    assert pick_num_splits(64, 8, 4096, 256) == 1
+    assert pick_num_splits(24, 2, 192, 256) == 1  # C1: capped by the short context
+    # long context, tiny batch: hundreds of splits (BASELINE C5 needs >= 256)
+    assert pick_num_splits(4, 8, 131072, 256) >= 16
+    for b, h, t in ((1, 1, 1), (1, 8, 5000), (32, 8, 16384), (4, 8, 131072), (3, 2, 0)):
+        s = pick_num_splits(b, h, t, 256)
+        assert 1 <= s <= _abi.PA_MAX_SPLITS
+
+
+def test_allocate_is_deterministic_and_well_formed():
+    a = allocate(LLAMA3_8B, 3, [5, 40, 17], device="cpu", seed=3, slack_blocks=4)
+    b = allocate(LLAMA3_8B, 3, [5, 40, 17], device="cpu", seed=3, slack_blocks=4)
+    assert torch.equal(a.k_cache, b.k_cache) and torch.equal(a.block_table, b.block_table)
+    nb = [1, 3, 2]
+    assert a.k_cache.shape == (sum(nb) + 4, 16, 8, 128)
+    used = torch.cat([a.block_table[i, :n] for i, n in enumerate(nb)])
+    assert used.unique().numel() == used.numel()  # each block used once
+    assert a.block_table[0, 1:].eq(0).all() and a.block_table[2, 2:].eq(0).all()
+    c = allocate(LLAMA3_8B, 1, [33], device="cpu", seed=4, shuffle=False)
+    assert c.block_table[0].tolist() == [0, 1, 2]
+
+
+def test_algorithmic_bytes_of_baseline_configs():
+    """BASELINE.md's per-call byte counts, from the same formula bench.py uses."""
+    import bench
+
+    def fake(shape, lens, kv, scale_dt=None):
+        meta = lambda dt: torch.empty(0, dtype=dt, device="meta")
+        st = {"fp16": torch.float16, "fp8_e5m2": torch.float8_e5m2, "int8": torch.int8}[kv]
+        return types.SimpleNamespace(shape=shape, block_size=16, kv_dtype=kv, k_cache=meta(st),
+                                     k_scale=meta(scale_dt) if scale_dt else None,
+                                     seq_lens=torch.tensor(lens))
+
+    assert bench._algorithmic_bytes(fake(LLAMA3_8B, [4096] * 64, "fp16")) == 1_074_855_936
+    assert bench._algorithmic_bytes(fake(LLAMA3_70B, [16384] * 32, "int8", torch.float32)) == 1_108_475_904
+    assert bench._algorithmic_bytes(fake(LLAMA3_8B, [131072] * 4, "fp16")) == 2_147_680_256

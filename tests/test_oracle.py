@@ -1,0 +1,445 @@
+"""CPU pinning of the oracle (oracle/reference.py) -- no GPU needed.
+
+The reference stores no golden vectors (its tests compute a live fp32 oracle,
+tests/test_correctness.py:59-122), so the torch oracle is pinned by:
+  * an independent float64 C restatement that walks pages (oracle/pa_oracle.c),
+    itself checked bit-for-bit on the fp16 / e5m2 decoders and the fp16
+    rounding against numpy and torch's conversions;
+  * closed forms (T = 1, q = 0, constant V, one dominant logit);
+  * torch SDPA's math backend on the gathered cache (reference.py:57-72);
+  * invariants (block-table permutation, split count, page size);
+  * quantisation identities (cache.py:33-62);
+  * committed fixtures under tests/golden/ (written by the C oracle);
+  * planted mistakes: mutated copies of the oracle must fail these checks.
+"""
+
+from __future__ import annotations
+
+import math
+import pathlib
+import types
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import c_oracle
+from oracle import reference as oracle
+from pagedattn import LLAMA3_8B, MHA_DEBUG, ModelShape, allocate
+from pagedattn.cache import PagedKVCache
+
+GOLDEN = pathlib.Path(__file__).resolve().parent / "golden"
+
+
+def _cache(shape, lens, kv_dtype="fp16", block_size=16, seed=0, scale_dtype=torch.float16,
+           shuffle=True, slack=0):
+    return allocate(shape, len(lens), lens, block_size=block_size, kv_dtype=kv_dtype,
+                    device="cpu", seed=seed, scale_dtype=scale_dtype, shuffle=shuffle,
+                    slack_blocks=slack)
+
+
+def _q(b, hq, d, seed):
+    g = torch.Generator().manual_seed(1000 + seed)
+    return torch.randn((b, hq, d), dtype=torch.float16, generator=g)
+
+
+def _dense_cache(shape, k_dense, v_dense, block_size=16, seed=0):
+    """PagedKVCache holding dense fp16 K/V [B, T, Hkv, D] under a permuted pool."""
+    b, t, h, d = k_dense.shape
+    nb_seq = -(-t // block_size)
+    pool = b * nb_seq + 3
+    perm = torch.randperm(pool, generator=torch.Generator().manual_seed(seed))
+    k = torch.zeros((pool, block_size, h, d), dtype=torch.float16)
+    v = torch.zeros_like(k)
+    bt = torch.zeros((b, nb_seq), dtype=torch.int32)
+    for bi in range(b):
+        for j in range(nb_seq):
+            phys = int(perm[bi * nb_seq + j])
+            bt[bi, j] = phys
+            lo, hi = j * block_size, min((j + 1) * block_size, t)
+            k[phys, : hi - lo] = k_dense[bi, lo:hi]
+            v[phys, : hi - lo] = v_dense[bi, lo:hi]
+    return PagedKVCache(shape, block_size, "fp16", k, v, None, None, bt,
+                        torch.full((b,), t, dtype=torch.int32))
+
+
+# --------------------------------------------------------------------------
+# the C oracle's own number decoders, against numpy / torch
+# --------------------------------------------------------------------------
+
+def test_c_half_decoder_all_patterns():
+    bits = np.arange(1 << 16, dtype=np.uint16)
+    want = bits.view(np.float16).astype(np.float64)
+    got = np.array([c_oracle.half_to_double(int(b)) for b in bits])
+    finite = np.isfinite(want)
+    assert np.array_equal(got[finite], want[finite])
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(np.isinf(got), np.isinf(want))
+
+
+def test_c_e5m2_decoder_all_bytes_and_shift_identity():
+    by = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    want = by.view(torch.float8_e5m2).to(torch.float64).numpy()
+    got = np.array([c_oracle.e5m2_to_double(int(b)) for b in range(256)])
+    fin = np.isfinite(want)
+    assert np.array_equal(got[fin], want[fin])
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    # e5m2 -> fp16 is the byte shifted into the high half (cache.py:27-28)
+    shifted = (by.to(torch.int32) << 8).to(torch.int16).view(torch.float16).to(torch.float64).numpy()
+    assert np.array_equal(shifted[fin], want[fin])
+
+
+def test_c_round_half_matches_numpy():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        rng.standard_normal(20000) * 10.0 ** rng.integers(-9, 5, 20000),
+        np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, 2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -26,
+                  1 + 2.0 ** -11, 1 + 3 * 2.0 ** -11]),
+    ])
+    want = x.astype(np.float16).astype(np.float64)
+    got = np.array([c_oracle.round_half(float(v)) for v in x])
+    assert np.array_equal(got, want)
+
+
+# --------------------------------------------------------------------------
+# torch oracle against the float64 C oracle
+# --------------------------------------------------------------------------
+
+CASES = [
+    # shape, lens, kv_dtype, block_size, scale dtype
+    (LLAMA3_8B, [1, 17, 300], "fp16", 16, torch.float16),
+    (ModelShape(14, 2, 64, "qwen"), [32, 192, 77, 5], "fp16", 16, torch.float16),
+    (MHA_DEBUG, [65, 130], "fp16", 32, torch.float16),
+    (ModelShape(8, 2, 32, "d32"), [40, 257], "fp8_e5m2", 16, torch.float16),
+    (LLAMA3_8B, [200, 33], "fp8_e5m2", 64, torch.float16),
+    (ModelShape(16, 2, 64, "g8"), [129, 3], "int8", 16, torch.float16),
+    (ModelShape(64, 8, 128, "70b"), [70], "int8", 16, torch.float32),
+    (ModelShape(24, 1, 256, "d256"), [50, 1], "int8", 32, torch.float32),
+]
+
+
+@pytest.mark.parametrize("shape,lens,kv_dtype,block_size,scale_dtype", CASES)
+def test_torch_oracle_matches_c_oracle(shape, lens, kv_dtype, block_size, scale_dtype):
+    c = _cache(shape, lens, kv_dtype, block_size, seed=len(lens), scale_dtype=scale_dtype, slack=5)
+    q = _q(len(lens), shape.num_q_heads, shape.head_dim, 1)
+    ref32 = oracle.reference_decode(q, c, out_dtype=torch.float32)
+    ref64 = c_oracle.decode(q, c)
+    assert (ref32.double() - ref64).abs().max().item() < 2e-5
+    # the reference's own output cast (reference.py:49)
+    assert oracle.reference_decode(q, c).dtype == torch.float16
+
+
+@pytest.mark.parametrize("sm_scale", [0.0, 0.01, 0.3])
+def test_sm_scale_override(sm_scale):
+    c = _cache(LLAMA3_8B, [90, 3], seed=3)
+    q = _q(2, 32, 128, 3)
+    got = oracle.reference_decode(q, c, sm_scale=sm_scale, out_dtype=torch.float32)
+    assert (got.double() - c_oracle.decode(q, c, sm_scale=sm_scale)).abs().max().item() < 2e-5
+
+
+# --------------------------------------------------------------------------
+# closed forms
+# --------------------------------------------------------------------------
+
+def _dequant_dense(c):
+    k, v = oracle.gather_contiguous(c)  # [B, Hkv, S, D] fp16
+    return k.float(), v.float()
+
+
+@pytest.mark.parametrize("kv_dtype", ["fp16", "fp8_e5m2", "int8"])
+def test_single_token_returns_v_row(kv_dtype):
+    c = _cache(LLAMA3_8B, [1, 1, 1], kv_dtype, seed=4)
+    q = _q(3, 32, 128, 4)
+    out = oracle.reference_decode(q, c, out_dtype=torch.float32)
+    _, v = _dequant_dense(c)
+    for h in range(32):
+        assert torch.equal(out[:, h], v[:, h // 4, 0])
+    assert torch.equal(c_oracle.decode(q, c).float(), out)
+
+
+def test_zero_query_gives_mean_of_v():
+    c = _cache(LLAMA3_8B, [37, 300], seed=5)
+    q = torch.zeros((2, 32, 128), dtype=torch.float16)
+    out = oracle.reference_decode(q, c, out_dtype=torch.float32)
+    _, v = _dequant_dense(c)
+    for bi, t in enumerate([37, 300]):
+        mean = v[bi, :, :t].double().mean(dim=1)  # [Hkv, D]
+        for h in range(32):
+            assert (out[bi, h].double() - mean[h // 4]).abs().max().item() < 1e-6
+    assert (c_oracle.decode(q, c) - out.double()).abs().max().item() < 1e-6
+
+
+def test_constant_v_and_dominant_logit():
+    g = torch.Generator().manual_seed(6)
+    b, t, h, d = 2, 50, 2, 64
+    shape = ModelShape(8, 2, 64, "t")
+    k = torch.randn((b, t, h, d), generator=g).half()
+    v = torch.full((b, t, h, d), 0.75, dtype=torch.float16)
+    c = _dense_cache(shape, k, v, seed=6)
+    q = _q(b, 8, d, 6)
+    out = oracle.reference_decode(q, c, out_dtype=torch.float32)
+    assert (out - 0.75).abs().max().item() < 1e-6
+    # one token whose key is a large multiple of q wins the softmax
+    v = torch.randn((b, t, h, d), generator=g).half()
+    q = torch.zeros((b, 8, d), dtype=torch.float16)
+    q[:, :, 0] = 1.0
+    k = torch.zeros((b, t, h, d), dtype=torch.float16)
+    k[:, 17, :, 0] = 400.0  # logit 50 vs 0 elsewhere
+    c = _dense_cache(shape, k, v, seed=7)
+    out = oracle.reference_decode(q, c, out_dtype=torch.float32)
+    for hq in range(8):
+        assert (out[:, hq] - v[:, 17, hq // 4].float()).abs().max().item() < 1e-12 + 1e-18
+    assert (c_oracle.decode(q, c).float() - out).abs().max().item() < 1e-6
+
+
+def test_query_head_reads_kv_head_h_div_group():
+    # kv head j holds the constant j: output of q head h must be h // group
+    b, t, hkv, d, g = 1, 40, 4, 32, 3
+    shape = ModelShape(hkv * g, hkv, d, "map")
+    k = torch.randn((b, t, hkv, d), generator=torch.Generator().manual_seed(8)).half()
+    v = torch.arange(hkv, dtype=torch.float16).view(1, 1, hkv, 1).expand(b, t, hkv, d).contiguous()
+    c = _dense_cache(shape, k, v, seed=8)
+    out = oracle.reference_decode(_q(b, hkv * g, d, 8), c, out_dtype=torch.float32)
+    for h in range(hkv * g):
+        assert torch.allclose(out[0, h], torch.full((d,), float(h // g)), atol=1e-6)
+
+
+# --------------------------------------------------------------------------
+# library routine, invariants, splits
+# --------------------------------------------------------------------------
+
+def test_sdpa_math_crosscheck():
+    c = _cache(LLAMA3_8B, [512, 100], seed=9)
+    q = _q(2, 32, 128, 9)
+    ref = oracle.reference_decode(q, c, out_dtype=torch.float32)
+    assert (oracle.sdpa_math_decode(q, c) - ref).abs().max().item() < 1e-5
+
+
+def test_block_permutation_invariance():
+    lens = [300, 45]
+    a = _cache(LLAMA3_8B, lens, seed=10, shuffle=False, slack=7)
+    q = _q(2, 32, 128, 10)
+    base = oracle.reference_decode(q, a, out_dtype=torch.float32)
+    perm = torch.randperm(a.k_cache.shape[0], generator=torch.Generator().manual_seed(2))
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(perm.numel())
+    moved = PagedKVCache(a.shape, a.block_size, a.kv_dtype, a.k_cache[perm], a.v_cache[perm],
+                         None, None, inv[a.block_table.long()].to(torch.int32), a.seq_lens)
+    assert torch.equal(oracle.reference_decode(q, moved, out_dtype=torch.float32), base)
+
+
+def test_page_size_invariance():
+    # the same logical K/V laid out in pages of 16, 32 and 64 tokens
+    g = torch.Generator().manual_seed(11)
+    k = torch.randn((2, 200, 8, 128), generator=g).half()
+    v = torch.randn((2, 200, 8, 128), generator=g).half()
+    q = _q(2, 32, 128, 11)
+    outs = [oracle.reference_decode(q, _dense_cache(LLAMA3_8B, k, v, bs, seed=bs),
+                                    out_dtype=torch.float32) for bs in (16, 32, 64)]
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
+def test_padding_positions_read_clamped_page():
+    # gather_contiguous pads shorter rows with the last block-table column
+    # (cache.py:200-205); masked positions must not change the result
+    c = _cache(LLAMA3_8B, [20, 70], seed=12)
+    k, _ = oracle.gather_contiguous(c)
+    assert k.shape == (2, 8, 70, 128)
+    bt = c.block_table
+    last = bt[0, bt.shape[1] - 1]
+    assert torch.equal(k[0, :, 64:70], c.k_cache[last, 0:6].permute(1, 0, 2))
+
+
+@pytest.mark.parametrize("num_splits", [1, 2, 3, 7, 40])
+def test_split_partials_merge_to_reference(num_splits):
+    lens = [1, 33, 500, 96]
+    c = _cache(LLAMA3_8B, lens, seed=13)
+    q = _q(4, 32, 128, 13)
+    part, lse = oracle.split_partials(q, c, num_splits, align=32)
+    cpart, clse = c_oracle.split(q, c, num_splits, align=32)
+    fin = torch.isfinite(clse)
+    assert torch.equal(torch.isfinite(lse), fin)
+    assert (lse.double()[fin] - clse[fin]).abs().max().item() < 1e-4
+    assert (part.double() - cpart).abs().max().item() < 2e-5
+    merged = oracle.split_merge(part, lse)
+    ref = c_oracle.decode(q, c)
+    assert (merged.double() - ref).abs().max().item() < 2e-5
+    # empty splits are exactly those that start at or past the sequence end
+    for bi, t in enumerate(lens):
+        ranges = oracle.split_ranges(t, num_splits, 32)
+        for s, (lo, hi) in enumerate(ranges):
+            assert bool(fin[bi, 0, s]) == (lo < hi)
+
+
+def test_split_ranges_closed_form():
+    # chunk = ceil(ceil(T/align)/S) * align (triton_decode.py:78-85)
+    assert oracle.split_ranges(100, 4, 32) == [(0, 32), (32, 64), (64, 96), (96, 100)]
+    assert oracle.split_ranges(100, 3, 32) == [(0, 64), (64, 100), (128, 100)]
+    assert oracle.split_ranges(4096, 8, 64) == [(512 * i, 512 * i + 512) for i in range(8)]
+
+
+def test_merge_of_all_empty_splits_is_nan():
+    part = torch.zeros((1, 1, 3, 4))
+    lse = torch.full((1, 1, 3), float("-inf"))
+    assert torch.isnan(oracle.split_merge(part, lse)).all()
+
+
+def test_empty_sequence_is_nan():
+    c = _cache(LLAMA3_8B, [0, 5], seed=14)
+    out = oracle.reference_decode(_q(2, 32, 128, 14), c, out_dtype=torch.float32)
+    assert torch.isnan(out[0]).all() and torch.isfinite(out[1]).all()
+
+
+# --------------------------------------------------------------------------
+# quantisation semantics (cache.py:33-62)
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("scale_dtype", [torch.float16, torch.float32])
+def test_int8_quant_roundtrip(scale_dtype):
+    x = torch.randn((64, 16, 8, 128), generator=torch.Generator().manual_seed(15)).half()
+    q, s = oracle.quantize_kv(x, "int8", scale_dtype)
+    assert q.dtype == torch.int8 and s.dtype == scale_dtype and s.shape == x.shape[:-1]
+    assert q.abs().max().item() <= 127
+    amax = x.abs().amax(-1).float().clamp_min(1e-6)
+    assert torch.equal(s, (amax / 127).to(scale_dtype))
+    deq = oracle.dequantize_kv(q, s, "int8").float()
+    half_step = s.float().unsqueeze(-1) / 2
+    # rounding error <= half a step, plus the fp16 rounding of the product
+    assert ((deq - x.float()).abs() <= half_step * 1.001 + deq.abs() * 2 ** -11 + 1e-7).all()
+
+
+def test_int8_dequant_rounds_product_once_to_fp16():
+    q = torch.tensor([[-127, -3, 0, 1, 77, 127]], dtype=torch.int8)
+    s = torch.tensor([0.0123], dtype=torch.float16)
+    got = oracle.dequantize_kv(q, s, "int8")
+    want = torch.tensor([[c_oracle.round_half(int(v) * float(s[0])) for v in q[0]]]).half()
+    assert torch.equal(got, want)
+
+
+def test_e5m2_quant_error_bound():
+    x = torch.randn(100000, generator=torch.Generator().manual_seed(16)).half()
+    q, s = oracle.quantize_kv(x, "fp8_e5m2")
+    assert s is None and q.dtype == torch.float8_e5m2
+    deq = oracle.dequantize_kv(q, None, "fp8_e5m2").float()
+    rel = ((deq - x.float()).abs() / x.float().abs().clamp_min(2 ** -14)).max().item()
+    assert rel <= 0.125 + 1e-6  # half an ulp of a 2-bit mantissa
+
+
+def test_oracle_quantize_matches_product():
+    from pagedattn.cache import quantize_kv as product_quantize
+
+    x = torch.randn((8, 16, 2, 64), generator=torch.Generator().manual_seed(17)).half()
+    for kv, sd in (("fp16", torch.float16), ("fp8_e5m2", torch.float16),
+                   ("int8", torch.float16), ("int8", torch.float32)):
+        a, sa = oracle.quantize_kv(x, kv, sd)
+        b, sb = product_quantize(x, kv, sd)
+        assert torch.equal(a.view(torch.uint8) if a.element_size() == 1 else a,
+                           b.view(torch.uint8) if b.element_size() == 1 else b)
+        assert (sa is None and sb is None) or torch.equal(sa, sb)
+
+
+def test_bytes_formula():
+    c = _cache(LLAMA3_8B, [100, 3], "int8", seed=18, scale_dtype=torch.float32)
+    assert oracle.bytes_read_per_decode_step(c) == 2 * 103 * 8 * 128 * 1 + 2 * 103 * 8 * 4
+    assert c.bytes_read_per_decode_step() == oracle.bytes_read_per_decode_step(c)
+
+
+# --------------------------------------------------------------------------
+# golden fixtures (tests/golden/make_golden.py, written by the C oracle)
+# --------------------------------------------------------------------------
+
+def _golden_files():
+    return sorted(GOLDEN.glob("*.npz"))
+
+
+def _cache_from_npz(z):
+    kv_dtype = str(z["kv_dtype"])
+    sd = {"fp16": torch.float16, "fp32": torch.float32}.get(str(z["scale_dtype"]))
+    store = {"fp16": torch.float16, "fp8_e5m2": torch.float8_e5m2, "int8": torch.int8}[kv_dtype]
+    as_t = lambda a, dt: torch.from_numpy(a.copy()).view(dt)
+    hq, hkv, d = (int(x) for x in z["heads"])
+    shape = ModelShape(hq, hkv, d, "golden")
+    k = as_t(z["k_cache"], store)
+    v = as_t(z["v_cache"], store)
+    ks = as_t(z["k_scale"], sd) if sd is not None else None
+    vs = as_t(z["v_scale"], sd) if sd is not None else None
+    c = PagedKVCache(shape, int(z["block_size"]), kv_dtype, k, v, ks, vs,
+                     torch.from_numpy(z["block_table"].copy()), torch.from_numpy(z["seq_lens"].copy()))
+    q = torch.from_numpy(z["q"].copy()).view(torch.float16)
+    return q, c
+
+
+def test_golden_fixtures_present():
+    assert len(_golden_files()) >= 4
+
+
+@pytest.mark.parametrize("path", _golden_files(), ids=lambda p: p.stem)
+def test_golden_fixture(path):
+    z = np.load(path, allow_pickle=False)
+    q, c = _cache_from_npz(z)
+    sm = float(z["sm_scale"])
+    want = torch.from_numpy(z["out"])
+    got = oracle.reference_decode(q, c, sm_scale=sm, out_dtype=torch.float32)
+    assert (got.double() - want).abs().max().item() < 2e-5
+    assert (c_oracle.decode(q, c, sm_scale=sm) - want).abs().max().item() < 1e-12
+    if "part" in z.files:
+        ns = int(z["num_splits"])
+        part, lse = oracle.split_partials(q, c, ns, align=32, sm_scale=sm)
+        assert (part.double() - torch.from_numpy(z["part"])).abs().max().item() < 2e-5
+        zl = torch.from_numpy(z["lse2"])
+        fin = torch.isfinite(zl)
+        assert torch.equal(torch.isfinite(lse), fin)
+        assert (lse.double()[fin] - zl[fin]).abs().max().item() < 1e-4
+
+
+# --------------------------------------------------------------------------
+# planted mistakes: each mutated oracle must fail the C-oracle comparison
+# --------------------------------------------------------------------------
+
+def _mutant(kind):
+    def decode(q, cache, sm_scale=None, out_dtype=None):
+        qc = q.float()
+        b, hq, d = qc.shape
+        hkv = cache.shape.num_kv_heads
+        group = hq // hkv
+        k, v = oracle.gather_contiguous(cache)
+        k, v = k.float(), v.float()
+        lens = cache.seq_lens.long()
+        s_max = k.shape[2]
+        valid = torch.arange(s_max).unsqueeze(0) < lens.unsqueeze(1)
+        if kind == "off_by_one_mask":
+            valid = torch.arange(s_max).unsqueeze(0) <= lens.unsqueeze(1)
+        scale = cache.shape.head_dim ** -0.5 if sm_scale is None else sm_scale
+        if kind == "no_scale":
+            scale = 1.0
+        out = torch.empty((b, hq, d))
+        for h in range(hq):
+            kvh = h % hkv if kind == "wrong_head_map" else h // group
+            logits = torch.einsum("bd,bsd->bs", qc[:, h], k[:, kvh]) * scale
+            logits = logits.masked_fill(~valid, float("-inf"))
+            p = torch.softmax(logits, dim=-1)
+            vv = k[:, kvh] if kind == "k_for_v" else v[:, kvh]
+            out[:, h] = torch.einsum("bs,bsd->bd", p, vv)
+        return out
+    return decode
+
+
+@pytest.mark.parametrize("kind", ["wrong_head_map", "no_scale", "off_by_one_mask", "k_for_v"])
+def test_planted_mistakes_are_caught(kind):
+    c = _cache(ModelShape(8, 4, 64, "m"), [40, 200], seed=19, slack=4)
+    q = _q(2, 8, 64, 19)
+    ref = c_oracle.decode(q, c)
+    honest = _mutant("none")(q, c)
+    assert (honest.double() - ref).abs().max().item() < 2e-5
+    bad = _mutant(kind)(q, c)
+    assert (bad.double() - ref).abs().max().item() > 1e-2
+
+
+def test_planted_dequant_mistake_is_caught():
+    # an int8 oracle that forgets the scale must fail against the C oracle
+    c = _cache(ModelShape(8, 2, 64, "m"), [60], "int8", seed=20)
+    q = _q(1, 8, 64, 20)
+    bad = types.SimpleNamespace(**{**c.__dict__, "k_scale": torch.ones_like(c.k_scale),
+                                   "v_scale": torch.ones_like(c.v_scale)})
+    got_bad = oracle.reference_decode(q, bad, out_dtype=torch.float32)
+    assert (got_bad.double() - c_oracle.decode(q, c)).abs().max().item() > 1e-1
