@@ -59,6 +59,13 @@ constexpr int kTile = 32;          // tokens per wave iteration
 constexpr float kRescaleLog2 = 8.0f;
 constexpr float kLog2e = 1.4426950408889634f;
 
+#ifndef PA_XCD_SWIZZLE
+#define PA_XCD_SWIZZLE 0
+#endif
+#ifndef PA_KV_NONTEMPORAL
+#define PA_KV_NONTEMPORAL 1
+#endif
+
 struct KParams {
   const uint8_t *q;
   const uint8_t *k;
@@ -142,25 +149,37 @@ __device__ __forceinline__ f16x8 fix_int8(f16x8 x) {
   }
 }
 
-// Load `BYTES` bytes (2, 4, 8, 16 or 32) into dwords `w`.
+// One K/V load. K and V are streamed exactly once per call, so they may be
+// fetched with the non-temporal hint to keep them from displacing reusable
+// lines in the caches.
+template <typename T>
+__device__ __forceinline__ T ld(const uint8_t *p) {
+#if PA_KV_NONTEMPORAL
+  return __builtin_nontemporal_load(reinterpret_cast<const T *>(p));
+#else
+  return *reinterpret_cast<const T *>(p);
+#endif
+}
+
+// Load `BYTES` bytes (2, 4, 8, 16 or 32) of K/V into dwords `w`.
 template <int BYTES>
 __device__ __forceinline__ void load_bytes(uint32_t *w, const uint8_t *p) {
   if constexpr (BYTES == 32) {
-    u32x4 a = *reinterpret_cast<const u32x4 *>(p);
-    u32x4 b = *reinterpret_cast<const u32x4 *>(p + 16);
+    u32x4 a = ld<u32x4>(p);
+    u32x4 b = ld<u32x4>(p + 16);
     w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
     w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
   } else if constexpr (BYTES == 16) {
-    u32x4 a = *reinterpret_cast<const u32x4 *>(p);
+    u32x4 a = ld<u32x4>(p);
     w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
   } else if constexpr (BYTES == 8) {
-    u32x2 a = *reinterpret_cast<const u32x2 *>(p);
+    u32x2 a = ld<u32x2>(p);
     w[0] = a.x; w[1] = a.y;
   } else if constexpr (BYTES == 4) {
-    w[0] = *reinterpret_cast<const uint32_t *>(p);
+    w[0] = ld<uint32_t>(p);
   } else {
     static_assert(BYTES == 2, "unsupported load width");
-    w[0] = *reinterpret_cast<const uint16_t *>(p);
+    w[0] = ld<uint16_t>(p);
   }
 }
 
@@ -398,6 +417,25 @@ __device__ __forceinline__ void tile_step(WaveState<KV, SC, D> &st, const KParam
   }
 }
 
+// The hardware deals workgroups round-robin to the 8 XCDs (physical index
+// p goes to XCD p % 8). Remap so that XCD x runs one contiguous range of
+// logical indices: all kv heads and splits of a few sequences then share one
+// XCD's L2 and TLBs, and the 8 head rows of each page (adjacent in the NHD
+// layout) are fetched by the same XCD. The tail beyond a multiple of 8 keeps
+// its index.
+__device__ __forceinline__ int xcd_logical(int p, int n) {
+#if PA_XCD_SWIZZLE
+  constexpr int kXcds = 8;
+  const int full = n - n % kXcds;
+  if (p >= full) return p;
+  const int per = full / kXcds;
+  return (p % kXcds) * per + p / kXcds;
+#else
+  (void)n;
+  return p;
+#endif
+}
+
 template <int KV, int SC, int D, bool SPLIT>
 __global__ void __launch_bounds__(kWaves * 64)
 paged_decode_kernel(const KParams p) {
@@ -413,8 +451,8 @@ paged_decode_kernel(const KParams p) {
   const int r16 = lane & 15;
   const int c = lane >> 4;
 
-  // blockIdx.x = ((b * hkv + kvh) * head_tiles + ht) * num_splits + split
-  int x = blockIdx.x;
+  // logical index = ((b * hkv + kvh) * head_tiles + ht) * num_splits + split
+  int x = xcd_logical(blockIdx.x, gridDim.x);
   const int split = x % p.num_splits;
   x /= p.num_splits;
   const int ht = x % p.head_tiles;
