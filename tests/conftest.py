@@ -8,7 +8,7 @@ import sys
 import pytest
 
 ROOT = pathlib.Path(__file__).resolve().parent.parent
-PKG = ROOT / "paged-decode-attention_amd"
+PKG = ROOT / "paged-decode-attention_amd"  # holds pagedattn/ and integration/
 for p in (str(PKG), str(ROOT)):
     if p not in sys.path:
         sys.path.insert(0, p)

@@ -1,0 +1,182 @@
+"""The vLLM V1 boundary (integration/vllm_backend.py) with stand-in vLLM
+classes: routing, shape gate, install() patching, env gating. CPU only; the
+GPU run of the same forward is in test_gpu_vllm.py."""
+
+from __future__ import annotations
+
+import types
+
+import pytest
+import torch
+
+from integration import vllm_backend as vb
+
+
+class FakeBaseImpl:
+    """Stands in for vLLM's TritonAttentionImpl: records delegated calls."""
+
+    def __init__(self, num_heads=32, num_kv_heads=8, head_size=128, **extra):
+        self.num_heads = num_heads
+        self.num_kv_heads = num_kv_heads
+        self.head_size = head_size
+        self.scale = head_size ** -0.5
+        self.kv_cache_dtype = "auto"
+        self.alibi_slopes = None
+        self.logits_soft_cap = 0
+        self.sliding_window = (-1, -1)
+        self.kv_sharing_target_layer_name = None
+        self.base_calls = 0
+        self.__dict__.update(extra)
+
+    def forward(self, layer, query, key, value, kv_cache, attn_metadata, output=None,
+                output_scale=None):
+        self.base_calls += 1
+        return "base"
+
+
+class FakeBaseBackend:
+    pass
+
+
+def _meta(**over):
+    m = types.SimpleNamespace(max_query_len=1, num_actual_tokens=2, use_cascade=False,
+                              local_attn_metadata=None, max_seq_len=300,
+                              block_table=torch.zeros((4, 20), dtype=torch.int32),
+                              seq_lens=torch.tensor([300, 5, 0, 0], dtype=torch.int32),
+                              slot_mapping=torch.tensor([299, 4], dtype=torch.int64))
+    m.__dict__.update(over)
+    return m
+
+
+def _kv(dtype=torch.float16, nb=8):
+    return torch.zeros((2, nb, 16, 8, 128), dtype=dtype)
+
+
+@pytest.fixture(autouse=True)
+def _reset_stats():
+    for k in vb.STATS:
+        vb.STATS[k] = 0
+    yield
+
+
+def test_supports_shape():
+    assert vb.supports_shape(32, 8, 128) == (True, "")
+    assert vb.supports_shape(14, 2, 64)[0]
+    assert not vb.supports_shape(30, 8, 128)[0]
+    assert not vb.supports_shape(32, 8, 96)[0]
+    assert not vb.supports_shape(32, 0, 128)[0]
+
+
+@pytest.mark.parametrize("impl_over,meta_over,kv,out,scale,expect", [
+    ({}, None, "kv", "out", None, "profiling run (no metadata)"),
+    ({}, {}, "kv", None, None, "no output buffer"),
+    ({}, {}, "kv", "out", 1.0, "fused output quantization"),
+    ({}, {}, "empty", "out", None, "empty kv cache"),
+    ({"kv_cache_dtype": "fp8_e4m3"}, {}, "kv", "out", None, "fp8 kv cache"),
+    ({"alibi_slopes": torch.ones(32)}, {}, "kv", "out", None, "alibi slopes"),
+    ({"logits_soft_cap": 30.0}, {}, "kv", "out", None, "logits soft cap"),
+    ({"sliding_window": (4095, 0)}, {}, "kv", "out", None, "sliding window"),
+    ({}, {"local_attn_metadata": object()}, "kv", "out", None, "local (iRoPE) attention"),
+    ({}, {"use_cascade": True}, "kv", "out", None, "cascade attention"),
+    ({}, {"max_query_len": 7}, "kv", "out", None, "not a pure-decode batch"),
+    ({}, {}, "bf16", "out", None, "cache dtype is not fp16"),
+    ({}, {}, "kv", "out", None, ""),
+])
+def test_reason_to_delegate(impl_over, meta_over, kv, out, scale, expect):
+    impl = FakeBaseImpl(**impl_over)
+    meta = None if meta_over is None else _meta(**meta_over)
+    kv_cache = {"kv": _kv(), "empty": torch.zeros(0), "bf16": _kv(torch.bfloat16)}[kv]
+    output = torch.zeros(2, 32, 128, dtype=torch.float16) if out else None
+    assert vb._reason_to_delegate(impl, meta, kv_cache, output, scale) == expect
+
+
+def test_forward_routes(monkeypatch):
+    Backend, Impl = vb.build_backend_classes(FakeBaseBackend, FakeBaseImpl)
+    assert Backend.get_name() == vb.BACKEND_NAME and Backend.get_impl_cls() is Impl
+    seen = []
+    monkeypatch.setattr(vb, "decode_forward", lambda *a: seen.append(a) or "ours")
+    q = torch.zeros(4, 32, 128, dtype=torch.float16)
+    out = torch.zeros_like(q)
+    impl = Impl()
+    assert impl.forward(None, q, q, q, _kv(), _meta(), out) == "ours"
+    assert len(seen) == 1
+    # prefill goes to vLLM
+    assert impl.forward(None, q, q, q, _kv(), _meta(max_query_len=5), out) == "base"
+    # unsupported head_dim goes to vLLM
+    odd = Impl(head_size=96)
+    assert odd.forward(None, q, q, q, _kv(), _meta(), out) == "base"
+    assert vb.STATS["delegated_calls"] == 2 and impl.base_calls == 1 and odd.base_calls == 1
+
+
+def test_decode_forward_builds_the_cache_view(monkeypatch):
+    monkeypatch.setattr(vb, "_cu_count", lambda dev: 256)
+    writes, calls = [], []
+
+    def fake_write(layer, impl, key, value, kc, vc, slots):
+        writes.append((kc.shape, vc.shape, slots.clone()))
+
+    def fake_decode(q, cache, out, num_splits, sm_scale):
+        calls.append(dict(q=q, cache=cache, out=out, num_splits=num_splits, sm_scale=sm_scale))
+
+    impl = FakeBaseImpl()
+    q = torch.randn(4, 32, 128).half()
+    output = torch.zeros_like(q)
+    kv = _kv()
+    meta = _meta()
+    res = vb.decode_forward(impl, None, q, q, q, kv, meta, output, write_kv=fake_write,
+                            decode=fake_decode)
+    assert res is output
+    assert writes[0][0] == (8, 16, 8, 128) and torch.equal(writes[0][2], meta.slot_mapping)
+    c = calls[0]
+    assert c["q"].shape == (2, 32, 128) and c["out"].data_ptr() == output.data_ptr()
+    cache = c["cache"]
+    assert cache.k_cache.data_ptr() == kv[0].data_ptr() and cache.v_cache.data_ptr() == kv[1].data_ptr()
+    assert cache.block_size == 16 and cache.kv_dtype == "fp16"
+    assert cache.block_table.shape[0] == 2 and torch.equal(cache.seq_lens, meta.seq_lens[:2])
+    assert (cache.shape.num_q_heads, cache.shape.num_kv_heads, cache.shape.head_dim) == (32, 8, 128)
+    assert c["num_splits"] == vb.pick_num_splits(2, 8, 300, 256)
+    assert c["sm_scale"] == impl.scale
+    assert vb.STATS == {"decode_calls": 1, "decode_tokens": 2, "delegated_calls": 0}
+    # a layer sharing another layer's KV does not write
+    impl.kv_sharing_target_layer_name = "model.layers.0.attn"
+    vb.decode_forward(impl, None, q, q, q, kv, meta, output, write_kv=fake_write, decode=fake_decode)
+    assert len(writes) == 1
+
+
+def test_install_patches_once():
+    class Platform:
+        @classmethod
+        def get_attn_backend_cls(cls, selected_backend, head_size, dtype, kv_cache_dtype,
+                                 block_size, use_v1, use_mla):
+            return "vllm.builtin.Backend"
+
+    assert vb.install(Platform) == vb.QUALNAME
+    assert Platform.get_attn_backend_cls(None, 128, torch.float16, "auto", 16, True, False) == vb.QUALNAME
+    assert Platform.get_attn_backend_cls(None, 128, torch.float16, "auto", 16, True, True) == "vllm.builtin.Backend"
+    assert Platform.get_attn_backend_cls(None, 128, torch.float16, "auto", 16, False, False) == "vllm.builtin.Backend"
+    patched = Platform.__dict__["get_attn_backend_cls"]
+    assert vb.install(Platform) == vb.QUALNAME
+    assert Platform.__dict__["get_attn_backend_cls"] is patched
+
+
+def test_maybe_install_from_env(monkeypatch):
+    class Platform:
+        @classmethod
+        def get_attn_backend_cls(cls, *a):
+            return "x"
+
+    monkeypatch.delenv("PAGEDATTN_VLLM_BACKEND", raising=False)
+    assert vb.maybe_install_from_env(Platform) is False
+    assert not getattr(Platform, "_pagedattn_patched", False)
+    monkeypatch.setenv("PAGEDATTN_VLLM_BACKEND", "1")
+    assert vb.maybe_install_from_env(Platform) is True
+    assert Platform._pagedattn_patched
+
+
+def test_qualname_resolves():
+    import importlib
+
+    mod_name, cls_name = vb.QUALNAME.rsplit(".", 1)
+    mod = importlib.import_module(mod_name)
+    assert mod is vb and hasattr(mod, cls_name)
+    assert (mod.PagedAttnTritonBackend is None) == (not vb.HAVE_VLLM)
