@@ -231,9 +231,10 @@ def main() -> int:
     # parity on a sample of sequences against the CPU oracle, and bit stability
     from oracle import reference as oracle
 
-    paged_decode_hip(q, cache, out=out, num_splits=splits)
+    msl = max(wl.lens)
+    paged_decode_hip(q, cache, out=out, num_splits=splits, max_seq_len=msl)
     first = out.clone()
-    paged_decode_hip(q, cache, out=out, num_splits=splits)
+    paged_decode_hip(q, cache, out=out, num_splits=splits, max_seq_len=msl)
     torch.cuda.synchronize()
     bit_stable = bool(torch.equal(first, out))
     rows = sorted({0, wl.batch // 2, wl.batch - 1})
@@ -254,13 +255,13 @@ def main() -> int:
 
     # whole-call timing (decode + reduce when split), rotating pool copies
     for i in range(args.warmup):
-        paged_decode_hip(q, caches[i % copies], out=out, num_splits=splits)
+        paged_decode_hip(q, caches[i % copies], out=out, num_splits=splits, max_seq_len=msl)
     torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     ev0.record()
     t_wall = time.perf_counter()
     for i in range(args.steps):
-        paged_decode_hip(q, caches[i % copies], out=out, num_splits=splits)
+        paged_decode_hip(q, caches[i % copies], out=out, num_splits=splits, max_seq_len=msl)
     ev1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_wall
@@ -270,7 +271,8 @@ def main() -> int:
     # the dominant kernel alone: the decode pass (partials when split)
     if splits > 1:
         part_out, part_lse = _WS.get(wl.batch, shape.num_q_heads, splits, shape.head_dim, dev)
-        run = lambda c: decode_partials(q, c, splits, part_out=part_out, part_lse=part_lse)
+        run = lambda c: decode_partials(q, c, splits, part_out=part_out, part_lse=part_lse,
+                                         max_seq_len=msl)
     else:
         run = lambda c: paged_decode_hip(q, c, out=out, num_splits=1)
     for i in range(args.warmup):

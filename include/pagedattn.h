@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define PA_ABI_VERSION 1
+#define PA_ABI_VERSION 2
 
 /* Return codes. */
 #define PA_OK 0
@@ -90,6 +90,14 @@ typedef struct pa_decode_args {
   int32_t num_blocks; /* pool size; block-table entries are clamped into it */
   int32_t max_blocks; /* block_table row length */
   int32_t num_splits; /* >= 1; > 1 selects the split-KV two-pass path */
+  /* Split chunking. 0: each sequence's range is cut into num_splits chunks of
+   * ceil(ceil(T_b/32)/num_splits)*32 tokens (the reference's per-sequence
+   * formula, pagedattn/triton_decode.py:78-85, with a 32-token unit).
+   * > 0: every sequence uses the chunk of a sequence of max_seq_len tokens,
+   * so a ragged batch's long sequences get all splits and short ones few
+   * (balanced work per workgroup); a sequence longer than max_seq_len falls
+   * back to its own per-sequence chunk, so no token is ever dropped. */
+  int32_t max_seq_len;
   /* element strides */
   int64_t stride_qb, stride_qh;
   int64_t stride_kn, stride_kt, stride_kh; /* shared by k_cache and v_cache */

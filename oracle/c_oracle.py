@@ -30,7 +30,7 @@ def _lib():
         common = [vp] * 7 + [i32] * 8 + [f64]
         lib.pa_oracle_decode.argtypes = common + [vp]
         lib.pa_oracle_decode.restype = i32
-        lib.pa_oracle_split.argtypes = common + [i32, i32, vp, vp]
+        lib.pa_oracle_split.argtypes = common + [i32, i32, i32, vp, vp]
         lib.pa_oracle_split.restype = i32
         lib.pa_oracle_half_to_double.argtypes = [ctypes.c_uint16]
         lib.pa_oracle_half_to_double.restype = f64
@@ -87,13 +87,14 @@ def decode(q: torch.Tensor, cache, sm_scale: float | None = None) -> torch.Tenso
     return torch.from_numpy(out)
 
 
-def split(q: torch.Tensor, cache, num_splits: int, align: int = 32, sm_scale: float | None = None):
+def split(q: torch.Tensor, cache, num_splits: int, align: int = 32, sm_scale: float | None = None,
+          max_seq_len: int = 0):
     """float64 per-split (normalised output [B,Hq,S,D], log2-sum-exp [B,Hq,S])."""
     args, keep = _args(q, cache, sm_scale)
     b, hq, d = q.shape
     part = np.zeros((b, hq, num_splits, d), dtype=np.float64)
     lse = np.zeros((b, hq, num_splits), dtype=np.float64)
-    rc = _lib().pa_oracle_split(*args, num_splits, align, _ptr(part), _ptr(lse))
+    rc = _lib().pa_oracle_split(*args, num_splits, align, max_seq_len, _ptr(part), _ptr(lse))
     assert rc == 0, "pa_oracle_split rejected its arguments"
     del keep
     return torch.from_numpy(part), torch.from_numpy(lse)

@@ -189,12 +189,13 @@ int pa_oracle_decode(const uint16_t *q, const void *k, const void *v, const void
 
 /* Per-split partials: part [B, Hq, S, D] (normalised output of the split) and
  * lse2 [B, Hq, S] = log2 of the split's sum of exp2(q.k * sm_scale * log2 e).
- * Split s covers [s*chunk, min((s+1)*chunk, T)), chunk = ceil(ceil(T/align)/S)*align. */
+ * Split s covers [s*chunk, min((s+1)*chunk, T)), chunk = ceil(ceil(T/align)/S)*align,
+ * or, with max_seq_len > 0, the larger of that and the chunk of max_seq_len. */
 int pa_oracle_split(const uint16_t *q, const void *k, const void *v, const void *ks,
                     const void *vs, const int32_t *bt, const int32_t *seq_lens, int batch,
                     int hq, int hkv, int d, int page, int max_blocks, int kv_dtype,
                     int scale_dtype, double sm_scale, int num_splits, int align,
-                    double *part, double *lse2) {
+                    int max_seq_len, double *part, double *lse2) {
   if (batch < 0 || hq <= 0 || hkv <= 0 || hq % hkv || d <= 0 || page <= 0 || num_splits < 1 ||
       align < 1)
     return -1;
@@ -215,11 +216,17 @@ int pa_oracle_split(const uint16_t *q, const void *k, const void *v, const void 
   for (int b = 0; b < batch; ++b) {
     const int T = seq_lens[b] > 0 ? seq_lens[b] : 0;
     const int64_t tiles = (T + align - 1) / align;
-    const int64_t chunk = ((tiles + num_splits - 1) / num_splits) * align;
+    int64_t chunk = ((tiles + num_splits - 1) / num_splits) * align;
+    if (max_seq_len > 0) { /* balanced mode: the longest sequence's chunk, never less than own */
+      const int64_t longest = ((int64_t)max_seq_len + align - 1) / align;
+      const int64_t c2 = ((longest + num_splits - 1) / num_splits) * align;
+      if (c2 > chunk) chunk = c2;
+    }
     for (int h = 0; h < hq; ++h) {
       load_q(q, ((int64_t)b * hq + h) * d, d, qrow);
       for (int s = 0; s < num_splits; ++s) {
         int64_t lo = s * chunk, hi = lo + chunk;
+        if (lo > T) lo = T;
         if (hi > T) hi = T;
         const int64_t idx = ((int64_t)b * hq + h) * num_splits + s;
         const double lse = attend(&c, qrow, b, h / group, (int)lo, (int)(lo < hi ? hi : lo),

@@ -135,13 +135,21 @@ def reference_decode(
     return out.to(q.dtype if out_dtype is None else out_dtype)
 
 
-def split_ranges(seq_len: int, num_splits: int, align: int) -> list[tuple[int, int]]:
+def split_ranges(seq_len: int, num_splits: int, align: int, max_seq_len: int = 0) -> list[tuple[int, int]]:
     """[lo, hi) of each split: chunk = ceil(ceil(T/align)/S)*align.
-    triton_decode.py:78-85 with the alignment unit as a parameter."""
-    chunk = -(-(-(-seq_len // align)) // num_splits) * align
+    triton_decode.py:78-85 with the alignment unit as a parameter.
+
+    With max_seq_len > 0 the chunk is sized from max_seq_len instead (but
+    never below the sequence's own chunk): the HIP build's balanced mode for
+    ragged batches. Ranges are clamped to [T, T) once past the end."""
+    def chunk_of(t):
+        return -(-(-(-t // align)) // num_splits) * align
+    chunk = chunk_of(seq_len)
+    if max_seq_len > 0:
+        chunk = max(chunk, chunk_of(max_seq_len))
     out = []
     for s in range(num_splits):
-        lo = s * chunk
+        lo = min(s * chunk, seq_len)
         out.append((lo, min(lo + chunk, seq_len)))
     return out
 
@@ -152,6 +160,7 @@ def split_partials(
     num_splits: int,
     align: int = 32,
     sm_scale: float | None = None,
+    max_seq_len: int = 0,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Per-split normalised output [B, Hq, S, D] and log2-sum-exp [B, Hq, S].
 
@@ -171,7 +180,7 @@ def split_partials(
     part = torch.zeros((b, hq, num_splits, d), dtype=torch.float32)
     lse = torch.full((b, hq, num_splits), float("-inf"), dtype=torch.float32)
     for bi in range(b):
-        for s, (lo, hi) in enumerate(split_ranges(lens[bi], num_splits, align)):
+        for s, (lo, hi) in enumerate(split_ranges(lens[bi], num_splits, align, max_seq_len)):
             if lo >= hi:
                 continue
             for h in range(hq):

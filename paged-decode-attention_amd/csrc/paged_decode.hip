@@ -13,6 +13,10 @@
 // through LDS at the end, so a workgroup is a split of kWaves sub-splits that
 // costs a single partial write.
 //
+// Each wave double-buffers its tiles in registers: the K/V loads of its next
+// tile are issued before the current tile is computed, so HBM requests stay in
+// flight while the MFMAs and the softmax run.
+//
 // Per 32-token tile (two 16-token sub-tiles, each inside one page because the
 // page size is a multiple of 16):
 //   S^T[tok, h] = K[tok, :] . Q[h, :]   v_mfma_f32_16x16x32_f16, A = K rows
@@ -23,9 +27,9 @@
 //                                        accumulator layout (no shuffles)
 // K rows are loaded in 16-byte pieces directly into the MFMA A-operand layout.
 // V rows are loaded in the natural [tok][d] layout, 16 lanes covering one row
-// contiguously, and transposed to [d][tok] pairs in registers with byte
-// permutes. All `group` query heads of a kv head share the tile (padded to the
-// 16 MFMA columns), so each K/V byte is read from HBM once.
+// contiguously, and transposed to [d][tok] pairs in registers with v_perm.
+// All `group` query heads of a kv head share the tile (padded to the 16 MFMA
+// columns), so each K/V byte is read from HBM once.
 //
 // Online softmax in the log2 domain as the reference (triton_decode.py:155-166)
 // with one change: the running maximum is only moved when a tile's maximum
@@ -33,10 +37,11 @@
 // on most tiles. This is exact algebra (the normaliser uses the same stale
 // maximum); probabilities stay <= 2^kRescaleLog2, far from fp16 overflow.
 //
-// Quantised KV is dequantised in registers:
+// Quantised KV is dequantised in registers with one v_perm per fp16 pair:
 //   fp8_e5m2 -> fp16: the e5m2 byte is the high byte of the fp16 pattern.
-//   int8 -> fp16 exactly (|x| <= 127), with the per-(token, head) scale folded
-//           into the fp32 score (K) and into the probability (V).
+//   int8 -> fp16 exactly (|x| <= 127): 0x64 | (b ^ 0x80) is 1152 + x as fp16,
+//           and 1152 is subtracted in fp16; the per-(token, head) scale is
+//           folded into the fp32 score (K) and into the probability (V).
 
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
@@ -58,13 +63,7 @@ constexpr int kWaves = 4;          // waves per workgroup
 constexpr int kTile = 32;          // tokens per wave iteration
 constexpr float kRescaleLog2 = 8.0f;
 constexpr float kLog2e = 1.4426950408889634f;
-
-#ifndef PA_XCD_SWIZZLE
-#define PA_XCD_SWIZZLE 0
-#endif
-#ifndef PA_KV_NONTEMPORAL
-#define PA_KV_NONTEMPORAL 1
-#endif
+constexpr uint32_t kInt8Xor = 0x64806480u;  // [b, 0, b', 0] -> [b ^ 0x80, 0x64, b' ^ 0x80, 0x64]
 
 struct KParams {
   const uint8_t *q;
@@ -77,7 +76,7 @@ struct KParams {
   float *part_lse;
   const int32_t *bt;
   const int32_t *seq_lens;
-  int32_t hkv, group, head_tiles, num_splits, num_blocks, max_blocks, log2_page;
+  int32_t hkv, group, head_tiles, num_splits, num_blocks, max_blocks, log2_page, max_seq_len;
   int64_t sqb, sqh;          // elements
   int64_t skn, skt, skh;     // bytes
   int64_t ssn, sst;          // bytes
@@ -96,97 +95,97 @@ struct RParams {
   int64_t spb, sph, sps, slb, slh, sob, soh;  // elements
 };
 
-__device__ __forceinline__ float wave_max16(float x) {
-  // max over the four lanes l, l^16, l^32, l^48 (same MFMA column)
-  x = fmaxf(x, __shfl_xor(x, 16));
-  x = fmaxf(x, __shfl_xor(x, 32));
-  return x;
+// Reductions over the four lanes l, l^16, l^32, l^48 that hold one MFMA
+// column (one query head). permlane16/32_swap hand each lane the values of
+// lane pairs (l, l^16) and (l, l^32); every lane of the column computes the
+// same expression, so the result is identical in all four.
+__device__ __forceinline__ float col_max(float x) {
+  const uint32_t xu = __float_as_uint(x);
+  const auto a = __builtin_amdgcn_permlane16_swap(xu, xu, false, false);
+  const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const uint32_t yu = __float_as_uint(y);
+  const auto b = __builtin_amdgcn_permlane32_swap(yu, yu, false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
-__device__ __forceinline__ float wave_sum16(float x) {
-  x += __shfl_xor(x, 16);
-  x += __shfl_xor(x, 32);
-  return x;
+__device__ __forceinline__ float col_sum(float x) {
+  const uint32_t xu = __float_as_uint(x);
+  const auto a = __builtin_amdgcn_permlane16_swap(xu, xu, false, false);
+  const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const uint32_t yu = __float_as_uint(y);
+  const auto b = __builtin_amdgcn_permlane32_swap(yu, yu, false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// 16-bit lane `s` of a packed array of fp16 values held in dwords.
-__device__ __forceinline__ uint32_t half_at(const uint32_t *w, int s) {
-  return (w[s >> 1] >> ((s & 1) * 16)) & 0xffffu;
+// v_perm_b32: byte k of the result is byte sel[k] of the 8 bytes {hi, lo}
+// (codes 0-3 pick `lo`, 4-7 pick `hi`, 0x0c gives 0x00).
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
-// Byte `s` of a packed byte array held in dwords.
-__device__ __forceinline__ uint32_t byte_at(const uint32_t *w, int s) {
-  return (w[s >> 2] >> ((s & 3) * 8)) & 0xffu;
-}
-
-// fp16 bit pattern of the value of one stored KV element.
-//   KV == PA_KV_FP8_E5M2: exact, the e5m2 byte is the high byte of the fp16.
-//   KV == PA_KV_INT8:     1024 + 128 + x as fp16 bits; the caller subtracts
-//                         1152 in fp16 afterwards, which is exact.
-template <int KV>
-__device__ __forceinline__ uint32_t byte_to_half_bits(uint32_t b) {
-  if constexpr (KV == PA_KV_FP8_E5M2) {
-    return b << 8;
-  } else {
-    return 0x6400u | (b ^ 0x80u);
-  }
-}
-
-__device__ __forceinline__ f16x8 bits_to_f16x8(uint32_t w0, uint32_t w1, uint32_t w2,
-                                               uint32_t w3) {
+__device__ __forceinline__ f16x8 as_f16x8(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
   u32x4 u = {w0, w1, w2, w3};
   return __builtin_bit_cast(f16x8, u);
 }
 
+// int8 operands hold 1152 + x; remove the offset (exact in fp16).
 template <int KV>
-__device__ __forceinline__ f16x8 fix_int8(f16x8 x) {
+__device__ __forceinline__ f16x8 finish(f16x8 x) {
   if constexpr (KV == PA_KV_INT8) {
     const _Float16 off = (_Float16)1152.0f;
-    f16x8 o = {off, off, off, off, off, off, off, off};
+    const f16x8 o = {off, off, off, off, off, off, off, off};
     return x - o;
   } else {
     return x;
   }
 }
 
-// One K/V load. K and V are streamed exactly once per call, so they may be
-// fetched with the non-temporal hint to keep them from displacing reusable
-// lines in the caches.
-template <typename T>
-__device__ __forceinline__ T ld(const uint8_t *p) {
-#if PA_KV_NONTEMPORAL
-  return __builtin_nontemporal_load(reinterpret_cast<const T *>(p));
-#else
-  return *reinterpret_cast<const T *>(p);
-#endif
-}
-
-// Load `BYTES` bytes (2, 4, 8, 16 or 32) of K/V into dwords `w`.
-template <int BYTES>
-__device__ __forceinline__ void load_bytes(uint32_t *w, const uint8_t *p) {
-  if constexpr (BYTES == 32) {
-    u32x4 a = ld<u32x4>(p);
-    u32x4 b = ld<u32x4>(p + 16);
-    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
-    w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
-  } else if constexpr (BYTES == 16) {
-    u32x4 a = ld<u32x4>(p);
-    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
-  } else if constexpr (BYTES == 8) {
-    u32x2 a = ld<u32x2>(p);
-    w[0] = a.x; w[1] = a.y;
-  } else if constexpr (BYTES == 4) {
-    w[0] = ld<uint32_t>(p);
+// Selector placing byte i of `lo` and byte j of `hi` into the two halves of a
+// dword: as the high byte (fp8 e5m2 -> fp16) or the low byte (int8, before the
+// kInt8Xor that turns [b, 0] into 0x64 | b ^ 0x80).
+template <int KV>
+__device__ __forceinline__ constexpr uint32_t pair_sel(uint32_t i, uint32_t j) {
+  if constexpr (KV == PA_KV_INT8) {
+    return i | (0x0cu << 8) | ((4u + j) << 16) | (0x0cu << 24);
   } else {
-    static_assert(BYTES == 2, "unsupported load width");
-    w[0] = ld<uint16_t>(p);
+    return 0x0cu | (i << 8) | (0x0cu << 16) | ((4u + j) << 24);
   }
 }
 
+// Two stored bytes -> two fp16 bit patterns (one v_perm, plus a xor for int8).
+template <int KV>
+__device__ __forceinline__ uint32_t bytes_to_halves(uint32_t hi, uint32_t lo, uint32_t sel) {
+  const uint32_t w = perm(hi, lo, sel);
+  if constexpr (KV == PA_KV_INT8) return w ^ kInt8Xor;
+  return w;
+}
+
+// One K/V load. K and V are streamed exactly once per call, so they are
+// fetched with the non-temporal hint.
+template <typename T>
+__device__ __forceinline__ T ldnt(const uint8_t *p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const T *>(p));
+}
+
 template <int BYTES>
-__device__ __forceinline__ void zero_words(uint32_t *w) {
-#pragma unroll
-  for (int i = 0; i < (BYTES + 3) / 4; ++i) w[i] = 0;
+__device__ __forceinline__ void load_bytes(uint32_t *w, const uint8_t *p) {
+  if constexpr (BYTES == 32) {
+    const u32x4 a = ldnt<u32x4>(p);
+    const u32x4 b = ldnt<u32x4>(p + 16);
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+    w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+  } else if constexpr (BYTES == 16) {
+    const u32x4 a = ldnt<u32x4>(p);
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+  } else if constexpr (BYTES == 8) {
+    const u32x2 a = ldnt<u32x2>(p);
+    w[0] = a.x; w[1] = a.y;
+  } else if constexpr (BYTES == 4) {
+    w[0] = ldnt<uint32_t>(p);
+  } else {
+    static_assert(BYTES == 2, "unsupported load width");
+    w[0] = ldnt<uint16_t>(p);
+  }
 }
 
 template <int SC>
@@ -209,8 +208,12 @@ struct Geo {
   // K piece loaded per lane: 16 B for fp16 (one k-step); for 1-byte types one
   // 16-byte piece covers two k-steps (8 B when head_dim == 32).
   static constexpr int kKPieceBytes = (kElem == 2) ? 16 : (D >= 64 ? 16 : 8);
+  static constexpr int kKPieceWords = kKPieceBytes / 4;
   static constexpr int kKStepsPerPiece = (kElem == 2) ? 1 : (D >= 64 ? 2 : 1);
   static constexpr int kKPieces = kKSteps / kKStepsPerPiece;
+  // double-buffer the tile registers unless they would crowd out the rest
+  static constexpr int kTileWords = 2 * kKPieces * kKPieceWords + 8 * kVWords;
+  static constexpr bool kPrefetch = kTileWords <= 64;
 };
 
 // Byte offset inside a K row of the piece read by lane group `c` for piece `j`.
@@ -240,7 +243,16 @@ __device__ __forceinline__ int q_dim_offset(int ks, int c) {
   }
 }
 
-template <int KV, int SC, int D>
+// Registers of one 32-token tile of one wave.
+template <int KV, int D>
+struct Tile {
+  using G = Geo<KV, D>;
+  uint32_t k[2][G::kKPieces][G::kKPieceWords];  // K rows, MFMA A layout
+  uint32_t v[8][G::kVWords];                    // V rows 4c+i (+16), elems kE*r16..
+  float sc;                                     // int8: one K or V scale per lane
+};
+
+template <int KV, int D>
 struct WaveState {
   using G = Geo<KV, D>;
   f16x8 qop[G::kKSteps];  // Q^T B-operands
@@ -249,81 +261,90 @@ struct WaveState {
   float l;                // running sum over this lane's tokens
 };
 
-// One 32-token tile for one wave. MASKED handles the range tail.
-template <int KV, int SC, int D, bool MASKED>
-__device__ __forceinline__ void tile_step(WaveState<KV, SC, D> &st, const KParams &p,
-                                          const int32_t *bt_row, int kvh, int n0, int hi,
-                                          int lane) {
+// Issue the loads of the tile starting at token n0 (< hi). Rows at or past
+// `hi` in the last tile are clamped to valid rows of the sequence: they are
+// read (finite data) and masked out of the softmax by compute_tile.
+template <int KV, int SC, int D>
+__device__ __forceinline__ void load_tile(Tile<KV, D> &r, const KParams &p, const int32_t *bt_row,
+                                          int kvh, int n0, int hi, int lane) {
   using G = Geo<KV, D>;
   const int r16 = lane & 15;
   const int c = lane >> 4;
   const int page_mask = (1 << p.log2_page) - 1;
+  const bool tail = n0 + kTile > hi;
 
-  // ---- block-table lookup: one entry per 16-token sub-tile (uniform) ----
   int64_t base[2];
+  int lim[2];
   int phys[2], off[2];
-  bool sub_live[2];
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
-    const int tok0 = n0 + 16 * u;
-    sub_live[u] = !MASKED || tok0 < hi;
-    phys[u] = 0;
-    off[u] = 0;
-    if (sub_live[u]) {
-      phys[u] = min(max(bt_row[tok0 >> p.log2_page], 0), p.num_blocks - 1);
-      off[u] = tok0 & page_mask;
-    }
+    int t0 = n0 + 16 * u;
+    if (tail) t0 = min(t0, (hi - 1) & ~15);  // a sub-tile past the end re-reads the last one
+    phys[u] = min(max(bt_row[t0 >> p.log2_page], 0), p.num_blocks - 1);
+    off[u] = t0 & page_mask;
+    lim[u] = hi - 1 - t0;  // last valid row of the sub-tile (>= 15 unless tail)
     base[u] = (int64_t)phys[u] * p.skn + (int64_t)off[u] * p.skt + (int64_t)kvh * p.skh;
   }
+  const uint32_t skt = (uint32_t)p.skt;
 
-  // ---- K: lane row = token (16u + r16), 16-byte pieces of the row ----
-  uint32_t kw[2][G::kKPieces][4];
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
-    const bool live = sub_live[u] && (!MASKED || (n0 + 16 * u + r16) < hi);
-    const uint8_t *row = p.k + base[u] + (int64_t)r16 * p.skt;
+    const uint8_t *kb = p.k + base[u];
+    const int rk = tail ? min(r16, lim[u]) : r16;
 #pragma unroll
-    for (int j = 0; j < G::kKPieces; ++j) {
-      if (live) {
-        load_bytes<G::kKPieceBytes>(kw[u][j], row + k_piece_offset<KV, D>(j, c));
-      } else {
-        zero_words<16>(kw[u][j]);
-      }
-    }
+    for (int j = 0; j < G::kKPieces; ++j)
+      load_bytes<G::kKPieceBytes>(r.k[u][j], kb + (uint32_t)rk * skt + k_piece_offset<KV, D>(j, c));
   }
-
-  // ---- V: lane (c, r16) reads tokens {4c+i, 16+4c+i}, elems [kE*r16, +kE) ----
-  uint32_t vw[8][G::kVWords];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const int u = e >> 2;
-    const int trow = 4 * c + (e & 3);
-    const bool live = sub_live[u] && (!MASKED || (n0 + 16 * u + trow) < hi);
-    const uint8_t *row = p.v + base[u] + (int64_t)trow * p.skt + G::kVBytes * r16;
-    if (live) {
-      load_bytes<G::kVBytes>(vw[e], row);
-    } else {
-      zero_words<G::kVBytes>(vw[e]);
-    }
+    const uint8_t *vb = p.v + base[u];
+    int rv = 4 * c + (e & 3);
+    if (tail) rv = min(rv, lim[u]);
+    load_bytes<G::kVBytes>(r.v[e], vb + (uint32_t)rv * skt + G::kVBytes * r16);
   }
+  if constexpr (KV == PA_KV_INT8) {
+    // lane -> (K or V, sub-tile, row): one coalesced scale load per tile
+    const int which = lane >> 5;
+    const int u = (lane >> 4) & 1;
+    const int row = tail ? min(r16, lim[u]) : r16;
+    const uint8_t *s = which ? p.vs : p.ks;
+    const int64_t so = (int64_t)phys[u] * p.ssn + (int64_t)(off[u] + row) * p.sst +
+                       (int64_t)kvh * (SC == PA_SCALE_FP32 ? 4 : 2);
+    r.sc = load_scale<SC>(s + so);
+  } else {
+    r.sc = 0.f;
+  }
+}
 
-  // ---- int8 scales for this lane's 8 tokens ----
+template <int KV, int SC, int D>
+__device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV, D> &r,
+                                             const KParams &p, int n0, int hi, int lane,
+                                             float *sc_lds) {
+  using G = Geo<KV, D>;
+  const int c = lane >> 4;
+  const bool tail = n0 + kTile > hi;
+
+  // ---- int8 scales of this lane's 8 tokens {4c+i, 16+4c+i} via LDS ----
   float ksc[8], vsc[8];
   if constexpr (KV == PA_KV_INT8) {
+    sc_lds[lane] = r.sc;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int u = e >> 2;
-      const int trow = 4 * c + (e & 3);
-      const bool live = sub_live[u] && (!MASKED || (n0 + 16 * u + trow) < hi);
-      ksc[e] = 0.f;
-      vsc[e] = 0.f;
-      if (live) {
-        const int64_t so = (int64_t)phys[u] * p.ssn + (int64_t)(off[u] + trow) * p.sst +
-                           (int64_t)kvh * (SC == PA_SCALE_FP32 ? 4 : 2);
-        ksc[e] = load_scale<SC>(p.ks + so);
-        vsc[e] = load_scale<SC>(p.vs + so);
+    for (int u = 0; u < 2; ++u) {
+      const f32x4 kq = *reinterpret_cast<const f32x4 *>(sc_lds + 16 * u + 4 * c);
+      const f32x4 vq = *reinterpret_cast<const f32x4 *>(sc_lds + 32 + 16 * u + 4 * c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ksc[4 * u + i] = kq[i];
+        vsc[4 * u + i] = vq[i];
       }
     }
+    // the next tile's scales overwrite the slot only after these reads
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
   }
 
   // ---- S^T = K Q^T ----
@@ -335,20 +356,17 @@ __device__ __forceinline__ void tile_step(WaveState<KV, SC, D> &st, const KParam
     for (int ks = 0; ks < G::kKSteps; ++ks) {
       f16x8 kop;
       if constexpr (G::kElem == 2) {
-        const uint32_t *w = kw[u][ks];
-        kop = bits_to_f16x8(w[0], w[1], w[2], w[3]);
+        const uint32_t *w = r.k[u][ks];
+        kop = as_f16x8(w[0], w[1], w[2], w[3]);
       } else {
         const int j = ks / G::kKStepsPerPiece;
         const int half = ks % G::kKStepsPerPiece;  // which 8 bytes of the piece
-        const uint32_t *w = kw[u][j] + 2 * half;
-        uint32_t h[4];
-#pragma unroll
-        for (int q2 = 0; q2 < 4; ++q2) {
-          const uint32_t b0 = byte_at(w, 2 * q2);
-          const uint32_t b1 = byte_at(w, 2 * q2 + 1);
-          h[q2] = byte_to_half_bits<KV>(b0) | (byte_to_half_bits<KV>(b1) << 16);
-        }
-        kop = fix_int8<KV>(bits_to_f16x8(h[0], h[1], h[2], h[3]));
+        const uint32_t w0 = r.k[u][j][2 * half];
+        const uint32_t w1 = r.k[u][j][2 * half + 1];
+        kop = finish<KV>(as_f16x8(bytes_to_halves<KV>(w0, w0, pair_sel<KV>(0, 1)),
+                                  bytes_to_halves<KV>(w0, w0, pair_sel<KV>(2, 3)),
+                                  bytes_to_halves<KV>(w1, w1, pair_sel<KV>(0, 1)),
+                                  bytes_to_halves<KV>(w1, w1, pair_sel<KV>(2, 3))));
       }
       a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, st.qop[ks], a, 0, 0, 0);
     }
@@ -361,19 +379,21 @@ __device__ __forceinline__ void tile_step(WaveState<KV, SC, D> &st, const KParam
   for (int e = 0; e < 8; ++e) {
     float x = sacc[e >> 2][e & 3] * p.qk_scale;
     if constexpr (KV == PA_KV_INT8) x *= ksc[e];
-    if constexpr (MASKED) {
-      const int tok = n0 + 16 * (e >> 2) + 4 * c + (e & 3);
-      if (tok >= hi) x = -INFINITY;
-    }
     s[e] = x;
   }
-  float tmax = s[0];
+  if (tail) {
 #pragma unroll
-  for (int e = 1; e < 8; ++e) tmax = fmaxf(tmax, s[e]);
-  tmax = wave_max16(tmax);
+    for (int e = 0; e < 8; ++e) {
+      const int tok = n0 + 16 * (e >> 2) + 4 * c + (e & 3);
+      if (tok >= hi) s[e] = -INFINITY;
+    }
+  }
+  float tmax = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])),
+                     fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+  tmax = col_max(tmax);
 
   const bool need = tmax > st.m + kRescaleLog2;
-  if (__builtin_amdgcn_ballot_w64(need) != 0) {
+  if (__builtin_expect(__builtin_amdgcn_ballot_w64(need) != 0, 0)) {
     const float m_new = need ? fmaxf(st.m, tmax) : st.m;
     const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
     st.l *= alpha;
@@ -383,13 +403,9 @@ __device__ __forceinline__ void tile_step(WaveState<KV, SC, D> &st, const KParam
   }
 
   float pr[8];
-  float lsum = 0.f;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    pr[e] = __builtin_amdgcn_exp2f(s[e] - st.m);
-    lsum += pr[e];
-  }
-  st.l += lsum;
+  for (int e = 0; e < 8; ++e) pr[e] = __builtin_amdgcn_exp2f(s[e] - st.m);
+  st.l += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
 
   f16x8 pop;
 #pragma unroll
@@ -405,39 +421,27 @@ __device__ __forceinline__ void tile_step(WaveState<KV, SC, D> &st, const KParam
     uint32_t h[4];
 #pragma unroll
     for (int m2 = 0; m2 < 4; ++m2) {
+      const uint32_t *lo = r.v[2 * m2];
+      const uint32_t *hi2 = r.v[2 * m2 + 1];
       if constexpr (G::kElem == 2) {
-        h[m2] = half_at(vw[2 * m2], sl) | (half_at(vw[2 * m2 + 1], sl) << 16);
+        const int wi = sl >> 1;
+        const uint32_t sel = (sl & 1) ? 0x07060302u : 0x05040100u;
+        h[m2] = perm(hi2[wi], lo[wi], sel);
       } else {
-        h[m2] = byte_to_half_bits<KV>(byte_at(vw[2 * m2], sl)) |
-                (byte_to_half_bits<KV>(byte_at(vw[2 * m2 + 1], sl)) << 16);
+        const int wi = sl >> 2;
+        const uint32_t b = sl & 3;
+        h[m2] = bytes_to_halves<KV>(hi2[wi], lo[wi], pair_sel<KV>(b, b));
       }
     }
-    const f16x8 vop = fix_int8<KV>(bits_to_f16x8(h[0], h[1], h[2], h[3]));
+    const f16x8 vop = finish<KV>(as_f16x8(h[0], h[1], h[2], h[3]));
     st.acc[sl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop, st.acc[sl], 0, 0, 0);
   }
 }
 
-// The hardware deals workgroups round-robin to the 8 XCDs (physical index
-// p goes to XCD p % 8). Remap so that XCD x runs one contiguous range of
-// logical indices: all kv heads and splits of a few sequences then share one
-// XCD's L2 and TLBs, and the 8 head rows of each page (adjacent in the NHD
-// layout) are fetched by the same XCD. The tail beyond a multiple of 8 keeps
-// its index.
-__device__ __forceinline__ int xcd_logical(int p, int n) {
-#if PA_XCD_SWIZZLE
-  constexpr int kXcds = 8;
-  const int full = n - n % kXcds;
-  if (p >= full) return p;
-  const int per = full / kXcds;
-  return (p % kXcds) * per + p / kXcds;
-#else
-  (void)n;
-  return p;
-#endif
-}
-
+// Two workgroups (8 waves) per CU must fit in the register file: the
+// double-buffered tiles are sized for that budget.
 template <int KV, int SC, int D, bool SPLIT>
-__global__ void __launch_bounds__(kWaves * 64)
+__global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
 paged_decode_kernel(const KParams p) {
   using G = Geo<KV, D>;
   constexpr int kRegs = 4 * G::kE;  // accumulator floats per lane
@@ -445,14 +449,15 @@ paged_decode_kernel(const KParams p) {
   __shared__ float sm_m[kWaves][16];
   __shared__ float sm_l[kWaves][16];
   __shared__ float sm_acc[kWaves - 1][kRegs][64];
+  __shared__ __attribute__((aligned(16))) float sm_sc[kWaves][64];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r16 = lane & 15;
   const int c = lane >> 4;
 
-  // logical index = ((b * hkv + kvh) * head_tiles + ht) * num_splits + split
-  int x = xcd_logical(blockIdx.x, gridDim.x);
+  // blockIdx.x = ((b * hkv + kvh) * head_tiles + ht) * num_splits + split
+  int x = blockIdx.x;
   const int split = x % p.num_splits;
   x /= p.num_splits;
   const int ht = x % p.head_tiles;
@@ -468,13 +473,22 @@ paged_decode_kernel(const KParams p) {
 
   int lo = 0, hi = seq_len;
   if (SPLIT) {
-    const int ntile_all = (seq_len + kTile - 1) / kTile;
-    const int chunk = ((ntile_all + p.num_splits - 1) / p.num_splits) * kTile;
-    lo = split * chunk;
-    hi = min(lo + chunk, seq_len);
+    // chunk = ceil(ceil(T / 32) / S) * 32 tokens, T = this sequence's length,
+    // or the batch's longest when max_seq_len is given (never shorter than
+    // the sequence's own chunk, so no token is dropped)
+    const int64_t own = ((int64_t)seq_len + kTile - 1) / kTile;
+    int64_t ntile_chunk = (own + p.num_splits - 1) / p.num_splits;
+    if (p.max_seq_len > 0) {
+      const int64_t longest = ((int64_t)p.max_seq_len + kTile - 1) / kTile;
+      ntile_chunk = max((longest + p.num_splits - 1) / p.num_splits, ntile_chunk);
+    }
+    const int64_t chunk = ntile_chunk * kTile;
+    const int64_t lo64 = min((int64_t)split * chunk, (int64_t)seq_len);
+    lo = (int)lo64;
+    hi = (int)min(lo64 + chunk, (int64_t)seq_len);
   }
 
-  WaveState<KV, SC, D> st;
+  WaveState<KV, D> st;
   st.m = -INFINITY;
   st.l = 0.f;
 #pragma unroll
@@ -492,18 +506,40 @@ paged_decode_kernel(const KParams p) {
   }
 
   const int32_t *bt_row = p.bt + (int64_t)b * p.sbtb;
+  float *sc_lds = sm_sc[wave];
   const int ntiles = (hi > lo) ? (hi - lo + kTile - 1) / kTile : 0;
-  for (int t = wave; t < ntiles; t += kWaves) {
-    const int n0 = lo + t * kTile;
-    if (n0 + kTile <= hi) {
-      tile_step<KV, SC, D, false>(st, p, bt_row, kvh, n0, hi, lane);
+  // this wave's tiles: wave + kWaves * i, i < cnt
+  const int cnt = ntiles > wave ? (ntiles - wave + kWaves - 1) / kWaves : 0;
+  auto n0_of = [&](int i) { return lo + (wave + kWaves * i) * kTile; };
+  if (cnt > 0) {
+    if constexpr (G::kPrefetch) {
+      Tile<KV, D> ta, tb;
+      load_tile<KV, SC, D>(ta, p, bt_row, kvh, n0_of(0), hi, lane);
+      int i = 0;
+      for (; i + 2 < cnt; i += 2) {
+        load_tile<KV, SC, D>(tb, p, bt_row, kvh, n0_of(i + 1), hi, lane);
+        compute_tile<KV, SC, D>(st, ta, p, n0_of(i), hi, lane, sc_lds);
+        load_tile<KV, SC, D>(ta, p, bt_row, kvh, n0_of(i + 2), hi, lane);
+        compute_tile<KV, SC, D>(st, tb, p, n0_of(i + 1), hi, lane, sc_lds);
+      }
+      if (i + 1 < cnt) {
+        load_tile<KV, SC, D>(tb, p, bt_row, kvh, n0_of(i + 1), hi, lane);
+        compute_tile<KV, SC, D>(st, ta, p, n0_of(i), hi, lane, sc_lds);
+        compute_tile<KV, SC, D>(st, tb, p, n0_of(i + 1), hi, lane, sc_lds);
+      } else {
+        compute_tile<KV, SC, D>(st, ta, p, n0_of(i), hi, lane, sc_lds);
+      }
     } else {
-      tile_step<KV, SC, D, true>(st, p, bt_row, kvh, n0, hi, lane);
+      for (int i = 0; i < cnt; ++i) {
+        Tile<KV, D> t;
+        load_tile<KV, SC, D>(t, p, bt_row, kvh, n0_of(i), hi, lane);
+        compute_tile<KV, SC, D>(st, t, p, n0_of(i), hi, lane, sc_lds);
+      }
     }
   }
 
   // ---- merge the waves through LDS ----
-  const float lw = wave_sum16(st.l);
+  const float lw = col_sum(st.l);
   if (c == 0) {
     sm_m[wave][r16] = st.m;
     sm_l[wave][r16] = lw;
@@ -580,46 +616,64 @@ paged_decode_kernel(const KParams p) {
 }
 
 // Merge of split partials, one wave per (b, h); lanes cover the head dim.
-// Fixed summation order, so repeated calls are bit-identical.
+// The split weights are computed once (lanes over splits) and shared through
+// LDS, then every lane walks the splits in a fixed order with 8 independent
+// loads in flight, so repeated calls are bit-identical.
+constexpr int kReduceChunk = 256;  // splits whose weights are staged at once
+
 template <int D>
 __global__ void __launch_bounds__(64) split_reduce_kernel(const RParams p) {
   constexpr int kPer = D / 64 > 0 ? D / 64 : 1;  // head-dim elements per lane
+  __shared__ float sw[kReduceChunk];
   const int lane = threadIdx.x;
   const int bh = blockIdx.x;
   const int b = bh / p.num_heads;
   const int h = bh % p.num_heads;
   const float *lse = p.part_lse + (int64_t)b * p.slb + (int64_t)h * p.slh;
   const float *part = p.part_out + (int64_t)b * p.spb + (int64_t)h * p.sph;
+  const int S = p.num_splits;
 
   float m = -INFINITY;
-  for (int s = lane; s < p.num_splits; s += 64) m = fmaxf(m, lse[s]);
+  for (int s = lane; s < S; s += 64) m = fmaxf(m, lse[s]);
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
 
-  float wsum = 0.f;
-  for (int s = lane; s < p.num_splits; s += 64) {
-    const float ls = lse[s];
-    wsum += (ls == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ls - m);
-  }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) wsum += __shfl_xor(wsum, o);
-
+  const bool active = lane * kPer < D;
   float acc[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) acc[i] = 0.f;
-  const bool active = lane * kPer < D;
-  if (m != -INFINITY) {
-    for (int s = 0; s < p.num_splits; ++s) {
-      const float ls = lse[s];
-      if (ls == -INFINITY) continue;
-      const float w = __builtin_amdgcn_exp2f(ls - m);
-      if (active) {
-        const float *src = part + (int64_t)s * p.sps + lane * kPer;
+  float wsum = 0.f;  // lane-local partial sums, combined in a fixed tree below
+  for (int s0 = 0; s0 < S; s0 += kReduceChunk) {
+    const int n = min(kReduceChunk, S - s0);
+    __syncthreads();
+    for (int s = lane; s < n; s += 64) {
+      const float ls = lse[s0 + s];
+      const float w = (ls == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ls - m);
+      sw[s] = w;
+      wsum += w;
+    }
+    __syncthreads();
+    if (active && m != -INFINITY) {
+      const float *src = part + (int64_t)s0 * p.sps + lane * kPer;
+      int s = 0;
+      for (; s + 8 <= n; s += 8) {
+        float v[8][kPer];
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) acc[i] += w * src[i];
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int i = 0; i < kPer; ++i) v[j][i] = src[(int64_t)(s + j) * p.sps + i];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int i = 0; i < kPer; ++i) acc[i] += sw[s + j] * v[j][i];
       }
+      for (; s < n; ++s)
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) acc[i] += sw[s] * src[(int64_t)s * p.sps + i];
     }
   }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) wsum += __shfl_xor(wsum, o);
   const float inv = (wsum > 0.f) ? 1.0f / wsum : 0.f;
   if (active) {
     _Float16 *dst = reinterpret_cast<_Float16 *>(p.out) + (int64_t)b * p.sob + (int64_t)h * p.soh + lane * kPer;
@@ -682,6 +736,9 @@ int build_params(const pa_decode_args *a, bool need_partials, KParams *kp) {
                 a->max_blocks);
   if (a->num_splits < 1 || a->num_splits > PA_MAX_SPLITS)
     return fail(PA_ERR_INVALID, "num_splits %d not in [1, %d]", a->num_splits, PA_MAX_SPLITS);
+  if (a->max_seq_len < 0) return fail(PA_ERR_INVALID, "max_seq_len %d < 0", a->max_seq_len);
+  if ((int64_t)a->max_blocks * a->block_size > 0x7fffffff)
+    return fail(PA_ERR_UNSUPPORTED, "max_blocks * block_size exceeds 2^31 tokens");
   if (a->io_dtype != PA_IO_FP16) return fail(PA_ERR_UNSUPPORTED, "io_dtype %d unsupported", a->io_dtype);
   if (a->kv_dtype != PA_KV_FP16 && a->kv_dtype != PA_KV_FP8_E5M2 && a->kv_dtype != PA_KV_INT8)
     return fail(PA_ERR_INVALID, "kv_dtype %d unknown", a->kv_dtype);
@@ -712,6 +769,7 @@ int build_params(const pa_decode_args *a, bool need_partials, KParams *kp) {
   if (!aligned(a->k_cache, 16) || !aligned(a->v_cache, 16) || (a->stride_kn * elem) % 16 ||
       (a->stride_kt * elem) % 16 || (a->stride_kh * elem) % 16)
     return fail(PA_ERR_INVALID, "k_cache/v_cache and their strides must be 16-byte aligned");
+  // in-page row offsets are 32-bit in the kernel
   if ((int64_t)a->block_size * a->stride_kt * elem >= (int64_t(1) << 31))
     return fail(PA_ERR_UNSUPPORTED, "page of %d tokens spans more than 2 GiB", a->block_size);
   if (need_partials) {
@@ -746,6 +804,7 @@ int build_params(const pa_decode_args *a, bool need_partials, KParams *kp) {
   k.num_blocks = a->num_blocks;
   k.max_blocks = a->max_blocks;
   k.log2_page = ilog2(a->block_size);
+  k.max_seq_len = a->max_seq_len;
   k.sqb = a->stride_qb;
   k.sqh = a->stride_qh;
   k.skn = a->stride_kn * elem;

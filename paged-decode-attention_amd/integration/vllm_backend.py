@@ -124,10 +124,12 @@ def decode_forward(impl, layer, query, key, value, kv_cache, attn_metadata, outp
         block_table=attn_metadata.block_table[:n],
         seq_lens=attn_metadata.seq_lens[:n],
     )
-    # max_seq_len is a host int in the metadata, so no device sync here
+    # max_seq_len is a host int in the metadata, so no device sync here; it
+    # also sizes the split chunks from the longest sequence (ragged balance)
     splits = pick_num_splits(n, impl.num_kv_heads, int(attn_metadata.max_seq_len),
                              _cu_count(query.device))
-    decode(query[:n], cache, out=output[:n], num_splits=splits, sm_scale=impl.scale)
+    decode(query[:n], cache, out=output[:n], num_splits=splits, sm_scale=impl.scale,
+           max_seq_len=int(attn_metadata.max_seq_len))
     STATS["decode_calls"] += 1
     STATS["decode_tokens"] += n
     return output

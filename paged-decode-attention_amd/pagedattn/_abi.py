@@ -12,7 +12,7 @@ import os
 import pathlib
 import threading
 
-PA_ABI_VERSION = 1
+PA_ABI_VERSION = 2
 
 PA_OK = 0
 PA_ERR_INVALID = -1
@@ -68,6 +68,7 @@ class PaDecodeArgs(ctypes.Structure):
         ("num_blocks", _i32),
         ("max_blocks", _i32),
         ("num_splits", _i32),
+        ("max_seq_len", _i32),
         ("stride_qb", _i64),
         ("stride_qh", _i64),
         ("stride_kn", _i64),

@@ -109,6 +109,7 @@ def _fill_args(
     sm_scale: float,
     part_out: torch.Tensor | None,
     part_lse: torch.Tensor | None,
+    max_seq_len: int = 0,
 ) -> _abi.PaDecodeArgs:
     b, hq, d = q.shape
     shape = cache.shape
@@ -157,6 +158,7 @@ def _fill_args(
     a.num_blocks = k.shape[0]
     a.max_blocks = bt.shape[1]
     a.num_splits = num_splits
+    a.max_seq_len = int(max_seq_len)
     a.stride_qb, a.stride_qh = q.stride(0), q.stride(1)
     a.stride_kn, a.stride_kt, a.stride_kh = k.stride(0), k.stride(1), k.stride(2)
     a.stride_ob, a.stride_oh = out.stride(0), out.stride(1)
@@ -203,6 +205,7 @@ def paged_decode_hip(
     num_warps: int = 4,
     num_stages: int = 3,
     sm_scale: float | None = None,
+    max_seq_len: int | None = None,
 ) -> torch.Tensor:
     """Paged GQA decode attention. q: [B, Hq, D] fp16 -> [B, Hq, D] fp16.
 
@@ -212,6 +215,14 @@ def paged_decode_hip(
     needs `seq_lens.max()` on the host (a device sync, as in the reference);
     serving callers pass `num_splits` to avoid it. A sequence with
     seq_len == 0 produces zeros.
+
+    `max_seq_len` (an addition; a host int such as vLLM's
+    `attn_metadata.max_seq_len`) sizes every sequence's split chunk from the
+    longest one, so a ragged batch gives its long sequences all the splits and
+    its short ones few. Without it each sequence is cut into `num_splits`
+    chunks of its own length (the reference's rule, triton_decode.py:78-85),
+    except when `num_splits=None`, where the longest length is known anyway.
+    Both rules compute the same attention.
     """
     del per_page_bt, num_warps, num_stages
     b, hq, d = q.shape
@@ -230,13 +241,15 @@ def paged_decode_hip(
     if num_splits is None:
         max_seq = int(cache.seq_lens.max().item())
         num_splits = pick_num_splits(b, hkv, max_seq, _cu_count(q.device), block_n)
+        if max_seq_len is None:
+            max_seq_len = max_seq
     num_splits = int(num_splits)
     scale = shape.softmax_scale if sm_scale is None else float(sm_scale)
 
     part_out = part_lse = None
     if num_splits > 1:
         part_out, part_lse = _WS.get(b, hq, num_splits, d, q.device)
-    args = _fill_args(q, cache, out, num_splits, scale, part_out, part_lse)
+    args = _fill_args(q, cache, out, num_splits, scale, part_out, part_lse, max_seq_len or 0)
     lib = _abi.load()
     with torch.cuda.device(q.device):
         rc = lib.pa_decode(ctypes.byref(args), _stream(q.device))
@@ -256,6 +269,7 @@ def decode_partials(
     sm_scale: float | None = None,
     part_out: torch.Tensor | None = None,
     part_lse: torch.Tensor | None = None,
+    max_seq_len: int = 0,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Run only the decode pass; returns (part_out [B,Hq,S,D], part_lse [B,Hq,S]).
 
@@ -270,7 +284,7 @@ def decode_partials(
     if part_lse is None:
         part_lse = torch.empty((b, hq, num_splits), dtype=torch.float32, device=q.device)
     out = torch.empty((b, hq, d), dtype=q.dtype, device=q.device)
-    args = _fill_args(q, cache, out, num_splits, scale, part_out, part_lse)
+    args = _fill_args(q, cache, out, num_splits, scale, part_out, part_lse, max_seq_len)
     lib = _abi.load()
     with torch.cuda.device(q.device):
         rc = lib.pa_decode_partials(ctypes.byref(args), _stream(q.device))

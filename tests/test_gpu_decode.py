@@ -95,13 +95,17 @@ def test_large_pages(block_size):
 
 
 def test_ragged_batch():
-    """test_correctness.py:81-90."""
+    """test_correctness.py:81-90, plus the balanced (max_seq_len) chunking."""
     lens = [7, 1, 4096, 513, 16, 2047, 64, 129]
     c = allocate(LLAMA3_8B, len(lens), lens, seed=3, device="cuda")
     q = seeded_q(len(lens), LLAMA3_8B.num_q_heads, LLAMA3_8B.head_dim, 3, device="cuda")
     ref = oracle.reference_decode(q, c, out_dtype=torch.float32)
     for ns in (1, 4):
         _check(paged_decode_hip(q, c, num_splits=ns), ref)
+    for ns in (3, 16, 130):
+        _check(paged_decode_hip(q, c, num_splits=ns, max_seq_len=max(lens)), ref)
+    # a max_seq_len below the true longest must not drop tokens
+    _check(paged_decode_hip(q, c, num_splits=8, max_seq_len=100), ref)
 
 
 def test_mha_group_one():
@@ -219,7 +223,17 @@ def test_vllm_style_strided_views():
     assert torch.equal(outbuf[3:], torch.zeros_like(outbuf[3:])), "wrote outside out"
 
 
-@pytest.mark.parametrize("kv_dtype", ["fp16", "int8"])
+def test_reduce_many_splits():
+    """The reduce kernel over more splits than it stages at once (256)."""
+    lens = [40000, 3]
+    c = allocate(LLAMA3_8B, 2, lens, seed=17, device="cuda")
+    q = seeded_q(2, 32, 128, 17, device="cuda")
+    ref = oracle.reference_decode(q, c, out_dtype=torch.float32)
+    _check(paged_decode_hip(q, c, num_splits=600, max_seq_len=max(lens)), ref)
+    _check(paged_decode_hip(q, c, num_splits=300), ref)
+
+
+@pytest.mark.parametrize("kv_dtype", ["fp16", "fp8_e5m2", "int8"])
 def test_bit_stable(kv_dtype):
     q, c = _qkv(4, 3000, seed=14, kv_dtype=kv_dtype)
     for ns in (1, 7):
@@ -230,15 +244,17 @@ def test_bit_stable(kv_dtype):
 
 
 @pytest.mark.parametrize("num_splits", [1, 3, 16])
-def test_split_partials_match_oracle(num_splits):
+@pytest.mark.parametrize("balanced", [False, True])
+def test_split_partials_match_oracle(num_splits, balanced):
     """The decode pass alone against the oracle's per-split restatement
     (triton_decode.py:169-188), and the reduce kernel against split_merge."""
     lens = [1, 100, 700]
     c = allocate(LLAMA3_8B, 3, lens, seed=15, device="cuda")
     q = seeded_q(3, 32, 128, 15, device="cuda")
-    po, pl = decode_partials(q, c, num_splits)
+    msl = max(lens) if balanced else 0
+    po, pl = decode_partials(q, c, num_splits, max_seq_len=msl)
     torch.cuda.synchronize()
-    ref_po, ref_pl = oracle.split_partials(q, c, num_splits, align=32)
+    ref_po, ref_pl = oracle.split_partials(q, c, num_splits, align=32, max_seq_len=msl)
     fin = torch.isfinite(ref_pl)
     assert torch.equal(torch.isfinite(pl.cpu()), fin), "empty-split pattern differs"
     assert (pl.cpu()[fin] - ref_pl[fin]).abs().max().item() < 1e-3

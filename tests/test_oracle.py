@@ -251,12 +251,14 @@ def test_padding_positions_read_clamped_page():
 
 
 @pytest.mark.parametrize("num_splits", [1, 2, 3, 7, 40])
-def test_split_partials_merge_to_reference(num_splits):
+@pytest.mark.parametrize("balanced", [False, True])
+def test_split_partials_merge_to_reference(num_splits, balanced):
     lens = [1, 33, 500, 96]
     c = _cache(LLAMA3_8B, lens, seed=13)
     q = _q(4, 32, 128, 13)
-    part, lse = oracle.split_partials(q, c, num_splits, align=32)
-    cpart, clse = c_oracle.split(q, c, num_splits, align=32)
+    msl = max(lens) if balanced else 0
+    part, lse = oracle.split_partials(q, c, num_splits, align=32, max_seq_len=msl)
+    cpart, clse = c_oracle.split(q, c, num_splits, align=32, max_seq_len=msl)
     fin = torch.isfinite(clse)
     assert torch.equal(torch.isfinite(lse), fin)
     assert (lse.double()[fin] - clse[fin]).abs().max().item() < 1e-4
@@ -266,7 +268,7 @@ def test_split_partials_merge_to_reference(num_splits):
     assert (merged.double() - ref).abs().max().item() < 2e-5
     # empty splits are exactly those that start at or past the sequence end
     for bi, t in enumerate(lens):
-        ranges = oracle.split_ranges(t, num_splits, 32)
+        ranges = oracle.split_ranges(t, num_splits, 32, msl)
         for s, (lo, hi) in enumerate(ranges):
             assert bool(fin[bi, 0, s]) == (lo < hi)
 
@@ -274,7 +276,11 @@ def test_split_partials_merge_to_reference(num_splits):
 def test_split_ranges_closed_form():
     # chunk = ceil(ceil(T/align)/S) * align (triton_decode.py:78-85)
     assert oracle.split_ranges(100, 4, 32) == [(0, 32), (32, 64), (64, 96), (96, 100)]
-    assert oracle.split_ranges(100, 3, 32) == [(0, 64), (64, 100), (128, 100)]
+    assert oracle.split_ranges(100, 3, 32) == [(0, 64), (64, 100), (100, 100)]
+    # balanced mode: the chunk of the longest sequence (never below its own)
+    assert oracle.split_ranges(100, 4, 32, max_seq_len=1000) == [(0, 100), (100, 100), (100, 100), (100, 100)]
+    assert oracle.split_ranges(1000, 4, 32, max_seq_len=1000) == oracle.split_ranges(1000, 4, 32)
+    assert oracle.split_ranges(2000, 4, 32, max_seq_len=1000) == oracle.split_ranges(2000, 4, 32)
     assert oracle.split_ranges(4096, 8, 64) == [(512 * i, 512 * i + 512) for i in range(8)]
 
 

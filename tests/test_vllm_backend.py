@@ -115,8 +115,9 @@ def test_decode_forward_builds_the_cache_view(monkeypatch):
     def fake_write(layer, impl, key, value, kc, vc, slots):
         writes.append((kc.shape, vc.shape, slots.clone()))
 
-    def fake_decode(q, cache, out, num_splits, sm_scale):
-        calls.append(dict(q=q, cache=cache, out=out, num_splits=num_splits, sm_scale=sm_scale))
+    def fake_decode(q, cache, out, num_splits, sm_scale, max_seq_len):
+        calls.append(dict(q=q, cache=cache, out=out, num_splits=num_splits, sm_scale=sm_scale,
+                          max_seq_len=max_seq_len))
 
     impl = FakeBaseImpl()
     q = torch.randn(4, 32, 128).half()
@@ -135,7 +136,7 @@ def test_decode_forward_builds_the_cache_view(monkeypatch):
     assert cache.block_table.shape[0] == 2 and torch.equal(cache.seq_lens, meta.seq_lens[:2])
     assert (cache.shape.num_q_heads, cache.shape.num_kv_heads, cache.shape.head_dim) == (32, 8, 128)
     assert c["num_splits"] == vb.pick_num_splits(2, 8, 300, 256)
-    assert c["sm_scale"] == impl.scale
+    assert c["sm_scale"] == impl.scale and c["max_seq_len"] == 300
     assert vb.STATS == {"decode_calls": 1, "decode_tokens": 2, "delegated_calls": 0}
     # a layer sharing another layer's KV does not write
     impl.kv_sharing_target_layer_name = "model.layers.0.attn"
