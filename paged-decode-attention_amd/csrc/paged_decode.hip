@@ -198,6 +198,14 @@ __device__ __forceinline__ float load_scale(const uint8_t *p) {
 }
 
 // Compile-time geometry for one (KV dtype, head_dim) instance.
+//
+// K is fetched in whole rows: consecutive lanes read consecutive 16-byte
+// pieces of a (token, kv_head) row, kKLanesPerRow lanes per row, so every
+// load instruction covers complete rows (as V's loads do). Rows arrive in a
+// per-wave LDS slot (padded by 16 bytes per row, which makes both the row
+// writes and the operand reads bank-conflict free) and are read back in the
+// MFMA A layout: lane (c, r) takes row r, head-dim elements [32*ks + 8*c, +8)
+// for k-step ks. Q uses the same mapping, which is all the reduction needs.
 template <int KV, int D>
 struct Geo {
   static constexpr int kElem = (KV == PA_KV_FP16) ? 2 : 1;  // stored bytes/elem
@@ -205,51 +213,24 @@ struct Geo {
   static constexpr int kE = D / 16;                         // V elems per lane row
   static constexpr int kVBytes = kE * kElem;                // V bytes per lane row
   static constexpr int kVWords = (kVBytes + 3) / 4;
-  // K piece loaded per lane: 16 B for fp16 (one k-step); for 1-byte types one
-  // 16-byte piece covers two k-steps (8 B when head_dim == 32).
-  static constexpr int kKPieceBytes = (kElem == 2) ? 16 : (D >= 64 ? 16 : 8);
-  static constexpr int kKPieceWords = kKPieceBytes / 4;
-  static constexpr int kKStepsPerPiece = (kElem == 2) ? 1 : (D >= 64 ? 2 : 1);
-  static constexpr int kKPieces = kKSteps / kKStepsPerPiece;
+  static constexpr int kRowBytes = D * kElem;               // one K/V row
+  static constexpr int kKLanesPerRow = kRowBytes / 16;      // 2 .. 32
+  static constexpr int kKRowsPerLoad = 64 / kKLanesPerRow;  // rows per instruction
+  static constexpr int kKLoads = kTile / kKRowsPerLoad;     // K loads per tile
+  static constexpr int kKSlotStride = kRowBytes + 16;       // padded LDS row
+  static constexpr int kKSlotBytes = kTile * kKSlotStride;  // per wave
   // double-buffer the tile registers unless they would crowd out the rest
-  static constexpr int kTileWords = 2 * kKPieces * kKPieceWords + 8 * kVWords;
+  static constexpr int kTileWords = 4 * kKLoads + 8 * kVWords;
   static constexpr bool kPrefetch = kTileWords <= 64;
 };
-
-// Byte offset inside a K row of the piece read by lane group `c` for piece `j`.
-// The head-dim index of element e of k-step `ks` for lane group c is
-//   2-byte types: 32*ks + 8*c + e
-//   1-byte types: 64*(ks/2) + 16*c + 8*(ks%2) + e   (head_dim >= 64)
-// Q is loaded with the same mapping, which is all the MFMA reduction needs.
-template <int KV, int D>
-__device__ __forceinline__ int k_piece_offset(int j, int c) {
-  using G = Geo<KV, D>;
-  if constexpr (G::kElem == 2) {
-    return (32 * j + 8 * c) * 2;
-  } else if constexpr (D >= 64) {
-    return 64 * j + 16 * c;
-  } else {
-    return 8 * c;
-  }
-}
-
-template <int KV, int D>
-__device__ __forceinline__ int q_dim_offset(int ks, int c) {
-  using G = Geo<KV, D>;
-  if constexpr (G::kElem == 2 || D < 64) {
-    return 32 * ks + 8 * c;
-  } else {
-    return 64 * (ks / 2) + 16 * c + 8 * (ks % 2);
-  }
-}
 
 // Registers of one 32-token tile of one wave.
 template <int KV, int D>
 struct Tile {
   using G = Geo<KV, D>;
-  uint32_t k[2][G::kKPieces][G::kKPieceWords];  // K rows, MFMA A layout
-  uint32_t v[8][G::kVWords];                    // V rows 4c+i (+16), elems kE*r16..
-  float sc;                                     // int8: one K or V scale per lane
+  u32x4 k[G::kKLoads];          // K: 16 bytes of row (i*rows_per_load + lane/lanes_per_row)
+  uint32_t v[8][G::kVWords];    // V rows 4c+i (+16), elems kE*r16..
+  float sc;                     // int8: one K or V scale per lane
 };
 
 template <int KV, int D>
@@ -288,12 +269,13 @@ __device__ __forceinline__ void load_tile(Tile<KV, D> &r, const KParams &p, cons
   const uint32_t skt = (uint32_t)p.skt;
 
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const uint8_t *kb = p.k + base[u];
-    const int rk = tail ? min(r16, lim[u]) : r16;
-#pragma unroll
-    for (int j = 0; j < G::kKPieces; ++j)
-      load_bytes<G::kKPieceBytes>(r.k[u][j], kb + (uint32_t)rk * skt + k_piece_offset<KV, D>(j, c));
+  for (int i = 0; i < G::kKLoads; ++i) {
+    const int row = i * G::kKRowsPerLoad + lane / G::kKLanesPerRow;  // 0..31
+    const int u = row >> 4;
+    int rr = row & 15;
+    if (tail) rr = min(rr, u ? lim[1] : lim[0]);
+    const uint8_t *kb = p.k + (u ? base[1] : base[0]);
+    r.k[i] = ldnt<u32x4>(kb + (uint32_t)rr * skt + 16 * (lane % G::kKLanesPerRow));
   }
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -320,10 +302,21 @@ __device__ __forceinline__ void load_tile(Tile<KV, D> &r, const KParams &p, cons
 template <int KV, int SC, int D>
 __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV, D> &r,
                                              const KParams &p, int n0, int hi, int lane,
-                                             float *sc_lds) {
+                                             float *sc_lds, uint8_t *k_lds) {
   using G = Geo<KV, D>;
+  const int r16 = lane & 15;
   const int c = lane >> 4;
   const bool tail = n0 + kTile > hi;
+
+  // ---- K rows -> LDS slot -> MFMA A layout ----
+#pragma unroll
+  for (int i = 0; i < G::kKLoads; ++i) {
+    const int row = i * G::kKRowsPerLoad + lane / G::kKLanesPerRow;
+    *reinterpret_cast<u32x4 *>(k_lds + row * G::kKSlotStride + 16 * (lane % G::kKLanesPerRow)) = r.k[i];
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
   // ---- int8 scales of this lane's 8 tokens {4c+i, 16+4c+i} via LDS ----
   float ksc[8], vsc[8];
@@ -355,14 +348,13 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
 #pragma unroll
     for (int ks = 0; ks < G::kKSteps; ++ks) {
       f16x8 kop;
+      const uint8_t *src = k_lds + (16 * u + r16) * G::kKSlotStride + (32 * ks + 8 * c) * G::kElem;
       if constexpr (G::kElem == 2) {
-        const uint32_t *w = r.k[u][ks];
-        kop = as_f16x8(w[0], w[1], w[2], w[3]);
+        kop = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4 *>(src));
       } else {
-        const int j = ks / G::kKStepsPerPiece;
-        const int half = ks % G::kKStepsPerPiece;  // which 8 bytes of the piece
-        const uint32_t w0 = r.k[u][j][2 * half];
-        const uint32_t w1 = r.k[u][j][2 * half + 1];
+        const u32x2 w = *reinterpret_cast<const u32x2 *>(src);
+        const uint32_t w0 = w.x;
+        const uint32_t w1 = w.y;
         kop = finish<KV>(as_f16x8(bytes_to_halves<KV>(w0, w0, pair_sel<KV>(0, 1)),
                                   bytes_to_halves<KV>(w0, w0, pair_sel<KV>(2, 3)),
                                   bytes_to_halves<KV>(w1, w1, pair_sel<KV>(0, 1)),
@@ -372,6 +364,9 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
     }
     sacc[u] = a;
   }
+  // the next tile's rows overwrite the slot only after these reads
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
 
   // ---- online softmax over the 8 tokens this lane holds for head r16 ----
   float s[8];
@@ -446,10 +441,15 @@ paged_decode_kernel(const KParams p) {
   using G = Geo<KV, D>;
   constexpr int kRegs = 4 * G::kE;  // accumulator floats per lane
 
+  // The K slots are only used inside the tile loop and the wave-merge buffer
+  // only after it (behind a barrier), so they share one allocation.
+  constexpr int kMergeBytes = (kWaves - 1) * kRegs * 64 * 4;
+  constexpr int kSlotsBytes = kWaves * G::kKSlotBytes;
+  __shared__ __attribute__((aligned(16))) uint8_t sm_raw[kMergeBytes > kSlotsBytes ? kMergeBytes : kSlotsBytes];
   __shared__ float sm_m[kWaves][16];
   __shared__ float sm_l[kWaves][16];
-  __shared__ float sm_acc[kWaves - 1][kRegs][64];
   __shared__ __attribute__((aligned(16))) float sm_sc[kWaves][64];
+  auto sm_acc = reinterpret_cast<float (*)[kRegs][64]>(sm_raw);
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -500,13 +500,14 @@ paged_decode_kernel(const KParams p) {
 #pragma unroll
     for (int ks = 0; ks < G::kKSteps; ++ks) {
       f16x8 qv = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (hv) qv = *reinterpret_cast<const f16x8 *>(qrow + q_dim_offset<KV, D>(ks, c));
+      if (hv) qv = *reinterpret_cast<const f16x8 *>(qrow + 32 * ks + 8 * c);
       st.qop[ks] = qv;
     }
   }
 
   const int32_t *bt_row = p.bt + (int64_t)b * p.sbtb;
   float *sc_lds = sm_sc[wave];
+  uint8_t *k_lds = sm_raw + wave * G::kKSlotBytes;
   const int ntiles = (hi > lo) ? (hi - lo + kTile - 1) / kTile : 0;
   // this wave's tiles: wave + kWaves * i, i < cnt
   const int cnt = ntiles > wave ? (ntiles - wave + kWaves - 1) / kWaves : 0;
@@ -518,22 +519,22 @@ paged_decode_kernel(const KParams p) {
       int i = 0;
       for (; i + 2 < cnt; i += 2) {
         load_tile<KV, SC, D>(tb, p, bt_row, kvh, n0_of(i + 1), hi, lane);
-        compute_tile<KV, SC, D>(st, ta, p, n0_of(i), hi, lane, sc_lds);
+        compute_tile<KV, SC, D>(st, ta, p, n0_of(i), hi, lane, sc_lds, k_lds);
         load_tile<KV, SC, D>(ta, p, bt_row, kvh, n0_of(i + 2), hi, lane);
-        compute_tile<KV, SC, D>(st, tb, p, n0_of(i + 1), hi, lane, sc_lds);
+        compute_tile<KV, SC, D>(st, tb, p, n0_of(i + 1), hi, lane, sc_lds, k_lds);
       }
       if (i + 1 < cnt) {
         load_tile<KV, SC, D>(tb, p, bt_row, kvh, n0_of(i + 1), hi, lane);
-        compute_tile<KV, SC, D>(st, ta, p, n0_of(i), hi, lane, sc_lds);
-        compute_tile<KV, SC, D>(st, tb, p, n0_of(i + 1), hi, lane, sc_lds);
+        compute_tile<KV, SC, D>(st, ta, p, n0_of(i), hi, lane, sc_lds, k_lds);
+        compute_tile<KV, SC, D>(st, tb, p, n0_of(i + 1), hi, lane, sc_lds, k_lds);
       } else {
-        compute_tile<KV, SC, D>(st, ta, p, n0_of(i), hi, lane, sc_lds);
+        compute_tile<KV, SC, D>(st, ta, p, n0_of(i), hi, lane, sc_lds, k_lds);
       }
     } else {
       for (int i = 0; i < cnt; ++i) {
         Tile<KV, D> t;
         load_tile<KV, SC, D>(t, p, bt_row, kvh, n0_of(i), hi, lane);
-        compute_tile<KV, SC, D>(st, t, p, n0_of(i), hi, lane, sc_lds);
+        compute_tile<KV, SC, D>(st, t, p, n0_of(i), hi, lane, sc_lds, k_lds);
       }
     }
   }
