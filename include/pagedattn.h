@@ -133,8 +133,12 @@ typedef struct pa_reduce_args {
  * num_splits == 1: one kernel writes `out` directly.
  * num_splits  > 1: the decode kernel writes per-split partials (normalised
  * output and log2-sum-exp) into part_out / part_lse, then the reduce kernel
- * merges them into `out`. A sequence with T_b == 0 yields zeros (the
- * reference yields NaN there). Replaces pagedattn/triton_decode.py:331-376. */
+ * merges them into `out`. Only splits that hold tokens do work: a sequence
+ * that fits in one split is written to `out` by the decode kernel and skipped
+ * by the merge, and the merge reads a sequence's non-empty splits only. (So
+ * part_out / part_lse are scratch here; pa_decode_partials fills them all.)
+ * A sequence with T_b == 0 yields zeros (the reference yields NaN there).
+ * Replaces pagedattn/triton_decode.py:331-376. */
 int pa_decode(const pa_decode_args *args, void *stream);
 
 /* Decode pass only: writes part_out / part_lse (num_splits >= 1) and skips

@@ -91,6 +91,8 @@ struct RParams {
   const float *part_out;
   const float *part_lse;
   uint8_t *out;
+  const int32_t *seq_lens;  // AUTO merge only
+  int32_t max_tokens, max_seq_len;  // AUTO merge only
   int32_t num_heads, num_splits;
   int64_t spb, sph, sps, slb, slh, sob, soh;  // elements
 };
@@ -433,9 +435,46 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
   }
 }
 
+// Token range [lo, hi) of one split, and how many of the sequence's splits
+// hold tokens. chunk = ceil(ceil(T / 32) / S) * 32 tokens, T = the sequence's
+// length (the reference's per-sequence rule, triton_decode.py:78-85), or the
+// chunk of a max_seq_len-token sequence when max_seq_len > 0 and that is
+// larger (ragged batches: long sequences take all S splits, short ones few;
+// never below the sequence's own chunk, so no token is dropped).
+struct SplitRange {
+  int lo, hi, n;
+};
+
+__device__ __forceinline__ SplitRange split_range(int seq_len, int num_splits, int max_seq_len,
+                                                  int split) {
+  const int64_t own = ((int64_t)seq_len + kTile - 1) / kTile;
+  int64_t ntile_chunk = (own + num_splits - 1) / num_splits;
+  if (max_seq_len > 0) {
+    const int64_t longest = ((int64_t)max_seq_len + kTile - 1) / kTile;
+    ntile_chunk = max((longest + num_splits - 1) / num_splits, ntile_chunk);
+  }
+  const int64_t chunk = max(ntile_chunk, (int64_t)1) * kTile;  // T = 0 still has one split
+  const int64_t lo = min((int64_t)split * chunk, (int64_t)seq_len);
+  SplitRange r;
+  r.lo = (int)lo;
+  r.hi = (int)min(lo + chunk, (int64_t)seq_len);
+  r.n = max(1, (int)((seq_len + chunk - 1) / chunk));
+  return r;
+}
+
+// What a workgroup does with its result:
+//   kUnsplit   one workgroup per (b, kv_head, head_tile): fp16 `out`
+//   kPartials  one per split: the normalised fp32 partial and its log2-sum-exp
+//              for every split, empty ones included (zeros, -inf): the
+//              reference's split epilogue (triton_decode.py:169-188)
+//   kAuto      as kPartials for the splits that hold tokens; a sequence that
+//              fits in one split writes `out` directly, empty splits return at
+//              once (the merge kernel skips both)
+enum { kUnsplit = 0, kPartials = 1, kAuto = 2 };
+
 // Two workgroups (8 waves) per CU must fit in the register file: the
 // double-buffered tiles are sized for that budget.
-template <int KV, int SC, int D, bool SPLIT>
+template <int KV, int SC, int D, int MODE>
 __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
 paged_decode_kernel(const KParams p) {
   using G = Geo<KV, D>;
@@ -472,20 +511,13 @@ paged_decode_kernel(const KParams p) {
   seq_len = max(0, min(seq_len, p.max_blocks << p.log2_page));
 
   int lo = 0, hi = seq_len;
-  if (SPLIT) {
-    // chunk = ceil(ceil(T / 32) / S) * 32 tokens, T = this sequence's length,
-    // or the batch's longest when max_seq_len is given (never shorter than
-    // the sequence's own chunk, so no token is dropped)
-    const int64_t own = ((int64_t)seq_len + kTile - 1) / kTile;
-    int64_t ntile_chunk = (own + p.num_splits - 1) / p.num_splits;
-    if (p.max_seq_len > 0) {
-      const int64_t longest = ((int64_t)p.max_seq_len + kTile - 1) / kTile;
-      ntile_chunk = max((longest + p.num_splits - 1) / p.num_splits, ntile_chunk);
-    }
-    const int64_t chunk = ntile_chunk * kTile;
-    const int64_t lo64 = min((int64_t)split * chunk, (int64_t)seq_len);
-    lo = (int)lo64;
-    hi = (int)min(lo64 + chunk, (int64_t)seq_len);
+  bool direct = true;  // write fp16 `out` (else a split partial)
+  if (MODE != kUnsplit) {
+    const SplitRange r = split_range(seq_len, p.num_splits, p.max_seq_len, split);
+    if (MODE == kAuto && split >= r.n) return;  // an empty split: nothing to read or write
+    lo = r.lo;
+    hi = r.hi;
+    direct = MODE == kAuto && r.n == 1;
   }
 
   WaveState<KV, D> st;
@@ -588,7 +620,7 @@ paged_decode_kernel(const KParams p) {
   if (r16 >= nh) return;
   const int h = qh0 + r16;
   const int d0 = 4 * G::kE * c;
-  if (SPLIT) {
+  if (!direct) {
     float *dst = p.part_out + (int64_t)b * p.spb + (int64_t)h * p.sph + (int64_t)split * p.sps + d0;
 #pragma unroll
     for (int v4 = 0; v4 < kRegs / 4; ++v4) {
@@ -622,7 +654,9 @@ paged_decode_kernel(const KParams p) {
 // loads in flight, so repeated calls are bit-identical.
 constexpr int kReduceChunk = 256;  // splits whose weights are staged at once
 
-template <int D>
+// AUTO: the partials of a kAuto decode; only the sequence's non-empty splits
+// are read, and sequences held by one split (already written) are skipped.
+template <int D, bool AUTO>
 __global__ void __launch_bounds__(64) split_reduce_kernel(const RParams p) {
   constexpr int kPer = D / 64 > 0 ? D / 64 : 1;  // head-dim elements per lane
   __shared__ float sw[kReduceChunk];
@@ -632,7 +666,12 @@ __global__ void __launch_bounds__(64) split_reduce_kernel(const RParams p) {
   const int h = bh % p.num_heads;
   const float *lse = p.part_lse + (int64_t)b * p.slb + (int64_t)h * p.slh;
   const float *part = p.part_out + (int64_t)b * p.spb + (int64_t)h * p.sph;
-  const int S = p.num_splits;
+  int S = p.num_splits;
+  if (AUTO) {
+    const int seq_len = max(0, min(p.seq_lens[b], p.max_tokens));
+    S = split_range(seq_len, p.num_splits, p.max_seq_len, 0).n;
+    if (S <= 1) return;
+  }
 
   float m = -INFINITY;
   for (int s = lane; s < S; s += 64) m = fmaxf(m, lse[s]);
@@ -827,33 +866,36 @@ int build_params(const pa_decode_args *a, bool need_partials, KParams *kp) {
 }
 
 template <int KV, int SC, int D>
-hipError_t launch_decode_t(const KParams &k, int grid, bool split, hipStream_t st) {
-  if (split) {
-    hipLaunchKernelGGL((paged_decode_kernel<KV, SC, D, true>), dim3(grid), dim3(kWaves * 64), 0, st, k);
+hipError_t launch_decode_t(const KParams &k, int grid, int mode, hipStream_t st) {
+  const dim3 g(grid), blk(kWaves * 64);
+  if (mode == kAuto) {
+    hipLaunchKernelGGL((paged_decode_kernel<KV, SC, D, kAuto>), g, blk, 0, st, k);
+  } else if (mode == kPartials) {
+    hipLaunchKernelGGL((paged_decode_kernel<KV, SC, D, kPartials>), g, blk, 0, st, k);
   } else {
-    hipLaunchKernelGGL((paged_decode_kernel<KV, SC, D, false>), dim3(grid), dim3(kWaves * 64), 0, st, k);
+    hipLaunchKernelGGL((paged_decode_kernel<KV, SC, D, kUnsplit>), g, blk, 0, st, k);
   }
   return hipGetLastError();
 }
 
 template <int KV, int SC>
-hipError_t launch_decode_d(const KParams &k, int d, int grid, bool split, hipStream_t st) {
+hipError_t launch_decode_d(const KParams &k, int d, int grid, int mode, hipStream_t st) {
   switch (d) {
-    case 32: return launch_decode_t<KV, SC, 32>(k, grid, split, st);
-    case 64: return launch_decode_t<KV, SC, 64>(k, grid, split, st);
-    case 128: return launch_decode_t<KV, SC, 128>(k, grid, split, st);
-    default: return launch_decode_t<KV, SC, 256>(k, grid, split, st);
+    case 32: return launch_decode_t<KV, SC, 32>(k, grid, mode, st);
+    case 64: return launch_decode_t<KV, SC, 64>(k, grid, mode, st);
+    case 128: return launch_decode_t<KV, SC, 128>(k, grid, mode, st);
+    default: return launch_decode_t<KV, SC, 256>(k, grid, mode, st);
   }
 }
 
-hipError_t launch_decode(const KParams &k, const pa_decode_args *a, bool split, hipStream_t st) {
+hipError_t launch_decode(const KParams &k, const pa_decode_args *a, int mode, hipStream_t st) {
   const int grid = a->batch * a->num_kv_heads * k.head_tiles * a->num_splits;
   const int d = a->head_dim;
-  if (a->kv_dtype == PA_KV_FP16) return launch_decode_d<PA_KV_FP16, PA_SCALE_NONE>(k, d, grid, split, st);
+  if (a->kv_dtype == PA_KV_FP16) return launch_decode_d<PA_KV_FP16, PA_SCALE_NONE>(k, d, grid, mode, st);
   if (a->kv_dtype == PA_KV_FP8_E5M2)
-    return launch_decode_d<PA_KV_FP8_E5M2, PA_SCALE_NONE>(k, d, grid, split, st);
-  if (a->scale_dtype == PA_SCALE_FP32) return launch_decode_d<PA_KV_INT8, PA_SCALE_FP32>(k, d, grid, split, st);
-  return launch_decode_d<PA_KV_INT8, PA_SCALE_FP16>(k, d, grid, split, st);
+    return launch_decode_d<PA_KV_FP8_E5M2, PA_SCALE_NONE>(k, d, grid, mode, st);
+  if (a->scale_dtype == PA_SCALE_FP32) return launch_decode_d<PA_KV_INT8, PA_SCALE_FP32>(k, d, grid, mode, st);
+  return launch_decode_d<PA_KV_INT8, PA_SCALE_FP16>(k, d, grid, mode, st);
 }
 
 int check_reduce(const pa_reduce_args *r, RParams *rp) {
@@ -874,6 +916,9 @@ int check_reduce(const pa_reduce_args *r, RParams *rp) {
   rp->part_out = r->part_out;
   rp->part_lse = r->part_lse;
   rp->out = static_cast<uint8_t *>(r->out);
+  rp->seq_lens = nullptr;
+  rp->max_tokens = 0;
+  rp->max_seq_len = 0;
   rp->num_heads = r->num_heads;
   rp->num_splits = r->num_splits;
   rp->spb = r->stride_pb;
@@ -886,13 +931,14 @@ int check_reduce(const pa_reduce_args *r, RParams *rp) {
   return PA_OK;
 }
 
+template <bool AUTO>
 hipError_t launch_reduce(const RParams &rp, int batch, int d, hipStream_t st) {
   const int grid = batch * rp.num_heads;
   switch (d) {
-    case 32: hipLaunchKernelGGL(split_reduce_kernel<32>, dim3(grid), dim3(64), 0, st, rp); break;
-    case 64: hipLaunchKernelGGL(split_reduce_kernel<64>, dim3(grid), dim3(64), 0, st, rp); break;
-    case 128: hipLaunchKernelGGL(split_reduce_kernel<128>, dim3(grid), dim3(64), 0, st, rp); break;
-    default: hipLaunchKernelGGL(split_reduce_kernel<256>, dim3(grid), dim3(64), 0, st, rp); break;
+    case 32: hipLaunchKernelGGL((split_reduce_kernel<32, AUTO>), dim3(grid), dim3(64), 0, st, rp); break;
+    case 64: hipLaunchKernelGGL((split_reduce_kernel<64, AUTO>), dim3(grid), dim3(64), 0, st, rp); break;
+    case 128: hipLaunchKernelGGL((split_reduce_kernel<128, AUTO>), dim3(grid), dim3(64), 0, st, rp); break;
+    default: hipLaunchKernelGGL((split_reduce_kernel<256, AUTO>), dim3(grid), dim3(64), 0, st, rp); break;
   }
   return hipGetLastError();
 }
@@ -936,13 +982,16 @@ int pa_decode(const pa_decode_args *a, void *stream) {
     ra = reduce_args_from(a);
     rc = check_reduce(&ra, &rp);
     if (rc != PA_OK) return rc;
+    rp.seq_lens = a->seq_lens;
+    rp.max_tokens = k.max_blocks << k.log2_page;
+    rp.max_seq_len = a->max_seq_len;
   }
   if (a->batch == 0) return ok();
   hipStream_t st = static_cast<hipStream_t>(stream);
-  hipError_t e = launch_decode(k, a, split, st);
+  hipError_t e = launch_decode(k, a, split ? kAuto : kUnsplit, st);
   if (e != hipSuccess) return fail(PA_ERR_HIP, "decode launch failed: %s", hipGetErrorString(e));
   if (split) {
-    e = launch_reduce(rp, a->batch, a->head_dim, st);
+    e = launch_reduce<true>(rp, a->batch, a->head_dim, st);
     if (e != hipSuccess) return fail(PA_ERR_HIP, "reduce launch failed: %s", hipGetErrorString(e));
   }
   return ok();
@@ -953,7 +1002,7 @@ int pa_decode_partials(const pa_decode_args *a, void *stream) {
   int rc = build_params(a, true, &k);
   if (rc != PA_OK) return rc;
   if (a->batch == 0) return ok();
-  hipError_t e = launch_decode(k, a, true, static_cast<hipStream_t>(stream));
+  hipError_t e = launch_decode(k, a, kPartials, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(PA_ERR_HIP, "decode launch failed: %s", hipGetErrorString(e));
   return ok();
 }
@@ -963,7 +1012,7 @@ int pa_split_reduce(const pa_reduce_args *r, void *stream) {
   int rc = check_reduce(r, &rp);
   if (rc != PA_OK) return rc;
   if (r->batch == 0) return ok();
-  hipError_t e = launch_reduce(rp, r->batch, r->head_dim, static_cast<hipStream_t>(stream));
+  hipError_t e = launch_reduce<false>(rp, r->batch, r->head_dim, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(PA_ERR_HIP, "reduce launch failed: %s", hipGetErrorString(e));
   return ok();
 }
