@@ -60,7 +60,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWaves = 4;          // waves per workgroup
-constexpr int kTile = 32;          // tokens per wave iteration
+constexpr int kSplitAlign = 32;    // split ranges are multiples of this many tokens
 constexpr float kRescaleLog2 = 8.0f;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr uint32_t kInt8Xor = 0x64806480u;  // [b, 0, b', 0] -> [b ^ 0x80, 0x64, b' ^ 0x80, 0x64]
@@ -216,23 +216,30 @@ struct Geo {
   static constexpr int kVBytes = kE * kElem;                // V bytes per lane row
   static constexpr int kVWords = (kVBytes + 3) / 4;
   static constexpr int kRowBytes = D * kElem;               // one K/V row
+  // A wave iteration covers kNSub 16-token sub-tiles (the code takes any
+  // even count). 64-token tiles for 128-byte rows (1-byte KV) were measured
+  // 1-3% slower than 32-token ones, so every geometry uses 2.
+  static constexpr int kNSub = 2;
+  static constexpr int kTT = 16 * kNSub;                    // tokens per tile
+  static constexpr int kVRows = 4 * kNSub;                  // V rows per lane
   static constexpr int kKLanesPerRow = kRowBytes / 16;      // 2 .. 32
   static constexpr int kKRowsPerLoad = 64 / kKLanesPerRow;  // rows per instruction
-  static constexpr int kKLoads = kTile / kKRowsPerLoad;     // K loads per tile
+  static constexpr int kKLoads = kTT / kKRowsPerLoad;       // K loads per tile
   static constexpr int kKSlotStride = kRowBytes + 16;       // padded LDS row
-  static constexpr int kKSlotBytes = kTile * kKSlotStride;  // per wave
+  static constexpr int kKSlotBytes = kTT * kKSlotStride;    // per wave
+  static constexpr int kScales = 2 * kTT;                   // int8: K and V scales per tile
   // double-buffer the tile registers unless they would crowd out the rest
-  static constexpr int kTileWords = 4 * kKLoads + 8 * kVWords;
+  static constexpr int kTileWords = 4 * kKLoads + kVRows * kVWords;
   static constexpr bool kPrefetch = kTileWords <= 64;
 };
 
-// Registers of one 32-token tile of one wave.
+// Registers of one tile of one wave.
 template <int KV, int D>
 struct Tile {
   using G = Geo<KV, D>;
-  u32x4 k[G::kKLoads];          // K: 16 bytes of row (i*rows_per_load + lane/lanes_per_row)
-  uint32_t v[8][G::kVWords];    // V rows 4c+i (+16), elems kE*r16..
-  float sc;                     // int8: one K or V scale per lane
+  u32x4 k[G::kKLoads];               // K: 16 bytes of row (i*rows_per_load + lane/lanes_per_row)
+  uint32_t v[G::kVRows][G::kVWords]; // V row 4c + (e & 3) of sub-tile e >> 2, elems kE*r16..
+  float sc[G::kScales / 64];         // int8: scale j*64 + lane of the tile's (K|V, sub-tile, row)
 };
 
 template <int KV, int D>
@@ -251,16 +258,17 @@ template <int KV, int SC, int D>
 __device__ __forceinline__ void load_tile(Tile<KV, D> &r, const KParams &p, const int32_t *bt_row,
                                           int kvh, int n0, int hi, int lane) {
   using G = Geo<KV, D>;
+  constexpr int NS = G::kNSub;
   const int r16 = lane & 15;
   const int c = lane >> 4;
   const int page_mask = (1 << p.log2_page) - 1;
-  const bool tail = n0 + kTile > hi;
+  const bool tail = n0 + G::kTT > hi;
 
-  int64_t base[2];
-  int lim[2];
-  int phys[2], off[2];
+  int64_t base[NS];
+  int lim[NS];
+  int phys[NS], off[NS];
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
+  for (int u = 0; u < NS; ++u) {
     int t0 = n0 + 16 * u;
     if (tail) t0 = min(t0, (hi - 1) & ~15);  // a sub-tile past the end re-reads the last one
     phys[u] = min(max(bt_row[t0 >> p.log2_page], 0), p.num_blocks - 1);
@@ -272,32 +280,49 @@ __device__ __forceinline__ void load_tile(Tile<KV, D> &r, const KParams &p, cons
 
 #pragma unroll
   for (int i = 0; i < G::kKLoads; ++i) {
-    const int row = i * G::kKRowsPerLoad + lane / G::kKLanesPerRow;  // 0..31
-    const int u = row >> 4;
+    const int row = i * G::kKRowsPerLoad + lane / G::kKLanesPerRow;  // 0 .. kTT-1
+    // the sub-tile is uniform per instruction unless one instruction spans two
+    const int u = G::kKRowsPerLoad <= 16 ? (i * G::kKRowsPerLoad) >> 4 : row >> 4;
+    int64_t b = base[0];
+    int lm = lim[0];
+#pragma unroll
+    for (int uu = 1; uu < NS; ++uu)
+      if (u == uu) {
+        b = base[uu];
+        lm = lim[uu];
+      }
     int rr = row & 15;
-    if (tail) rr = min(rr, u ? lim[1] : lim[0]);
-    const uint8_t *kb = p.k + (u ? base[1] : base[0]);
-    r.k[i] = ldnt<u32x4>(kb + (uint32_t)rr * skt + 16 * (lane % G::kKLanesPerRow));
+    if (tail) rr = min(rr, lm);
+    r.k[i] = ldnt<u32x4>(p.k + b + (uint32_t)rr * skt + 16 * (lane % G::kKLanesPerRow));
   }
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
+  for (int e = 0; e < G::kVRows; ++e) {
     const int u = e >> 2;
-    const uint8_t *vb = p.v + base[u];
     int rv = 4 * c + (e & 3);
     if (tail) rv = min(rv, lim[u]);
-    load_bytes<G::kVBytes>(r.v[e], vb + (uint32_t)rv * skt + G::kVBytes * r16);
+    load_bytes<G::kVBytes>(r.v[e], p.v + base[u] + (uint32_t)rv * skt + G::kVBytes * r16);
   }
   if constexpr (KV == PA_KV_INT8) {
-    // lane -> (K or V, sub-tile, row): one coalesced scale load per tile
-    const int which = lane >> 5;
-    const int u = (lane >> 4) & 1;
-    const int row = tail ? min(r16, lim[u]) : r16;
-    const uint8_t *s = which ? p.vs : p.ks;
-    const int64_t so = (int64_t)phys[u] * p.ssn + (int64_t)(off[u] + row) * p.sst +
-                       (int64_t)kvh * (SC == PA_SCALE_FP32 ? 4 : 2);
-    r.sc = load_scale<SC>(s + so);
-  } else {
-    r.sc = 0.f;
+    // value j*64 + lane -> (K or V, sub-tile, row): coalesced scale loads
+#pragma unroll
+    for (int j = 0; j < G::kScales / 64; ++j) {
+      const int vi = j * 64 + lane;
+      const int which = vi / (16 * NS);
+      const int u = (vi >> 4) % NS;
+      int ph = phys[0], of = off[0], lm = lim[0];
+#pragma unroll
+      for (int uu = 1; uu < NS; ++uu)
+        if (u == uu) {
+          ph = phys[uu];
+          of = off[uu];
+          lm = lim[uu];
+        }
+      const int row = tail ? min(r16, lm) : r16;
+      const uint8_t *sp = which ? p.vs : p.ks;
+      const int64_t so = (int64_t)ph * p.ssn + (int64_t)(of + row) * p.sst +
+                         (int64_t)kvh * (SC == PA_SCALE_FP32 ? 4 : 2);
+      r.sc[j] = load_scale<SC>(sp + so);
+    }
   }
 }
 
@@ -306,9 +331,11 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
                                              const KParams &p, int n0, int hi, int lane,
                                              float *sc_lds, uint8_t *k_lds) {
   using G = Geo<KV, D>;
+  constexpr int NS = G::kNSub;
+  constexpr int NV = 4 * NS;  // scores per lane: tokens 16u + 4c + i
   const int r16 = lane & 15;
   const int c = lane >> 4;
-  const bool tail = n0 + kTile > hi;
+  const bool tail = n0 + G::kTT > hi;
 
   // ---- K rows -> LDS slot -> MFMA A layout ----
 #pragma unroll
@@ -320,17 +347,18 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  // ---- int8 scales of this lane's 8 tokens {4c+i, 16+4c+i} via LDS ----
-  float ksc[8], vsc[8];
+  // ---- int8 scales of this lane's tokens {16u + 4c + i} via LDS ----
+  float ksc[NV], vsc[NV];
   if constexpr (KV == PA_KV_INT8) {
-    sc_lds[lane] = r.sc;
+#pragma unroll
+    for (int j = 0; j < G::kScales / 64; ++j) sc_lds[j * 64 + lane] = r.sc[j];
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < NS; ++u) {
       const f32x4 kq = *reinterpret_cast<const f32x4 *>(sc_lds + 16 * u + 4 * c);
-      const f32x4 vq = *reinterpret_cast<const f32x4 *>(sc_lds + 32 + 16 * u + 4 * c);
+      const f32x4 vq = *reinterpret_cast<const f32x4 *>(sc_lds + 16 * (NS + u) + 4 * c);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         ksc[4 * u + i] = kq[i];
@@ -342,10 +370,10 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
     __builtin_amdgcn_wave_barrier();
   }
 
-  // ---- S^T = K Q^T ----
-  f32x4 sacc[2];
+  // ---- S^T = K Q^T, one 16-token sub-tile at a time ----
+  f32x4 sacc[NS];
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
+  for (int u = 0; u < NS; ++u) {
     f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < G::kKSteps; ++ks) {
@@ -370,23 +398,24 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
 
-  // ---- online softmax over the 8 tokens this lane holds for head r16 ----
-  float s[8];
+  // ---- online softmax over the tokens this lane holds for head r16 ----
+  float s[NV];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
+  for (int e = 0; e < NV; ++e) {
     float x = sacc[e >> 2][e & 3] * p.qk_scale;
     if constexpr (KV == PA_KV_INT8) x *= ksc[e];
     s[e] = x;
   }
   if (tail) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
+    for (int e = 0; e < NV; ++e) {
       const int tok = n0 + 16 * (e >> 2) + 4 * c + (e & 3);
       if (tok >= hi) s[e] = -INFINITY;
     }
   }
-  float tmax = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])),
-                     fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+  float tmax = s[0];
+#pragma unroll
+  for (int e = 1; e < NV; ++e) tmax = fmaxf(tmax, s[e]);
   tmax = col_max(tmax);
 
   const bool need = tmax > st.m + kRescaleLog2;
@@ -399,39 +428,44 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
     st.m = m_new;
   }
 
-  float pr[8];
+  float pr[NV];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) pr[e] = __builtin_amdgcn_exp2f(s[e] - st.m);
-  st.l += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
+  for (int e = 0; e < NV; ++e) pr[e] = __builtin_amdgcn_exp2f(s[e] - st.m);
+  float lsum = 0.f;
+#pragma unroll
+  for (int e = 0; e < NV; e += 4) lsum += (pr[e] + pr[e + 1]) + (pr[e + 2] + pr[e + 3]);
+  st.l += lsum;
 
-  f16x8 pop;
+  // ---- O^T += V^T P^T: one MFMA per d-slab and pair of sub-tiles ----
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    float x = pr[e];
-    if constexpr (KV == PA_KV_INT8) x *= vsc[e];
-    pop[e] = (_Float16)x;
-  }
-
-  // ---- O^T += V^T P^T, one MFMA per d-slab ----
+  for (int pp = 0; pp < NS / 2; ++pp) {
+    f16x8 pop;
 #pragma unroll
-  for (int sl = 0; sl < G::kE; ++sl) {
-    uint32_t h[4];
-#pragma unroll
-    for (int m2 = 0; m2 < 4; ++m2) {
-      const uint32_t *lo = r.v[2 * m2];
-      const uint32_t *hi2 = r.v[2 * m2 + 1];
-      if constexpr (G::kElem == 2) {
-        const int wi = sl >> 1;
-        const uint32_t sel = (sl & 1) ? 0x07060302u : 0x05040100u;
-        h[m2] = perm(hi2[wi], lo[wi], sel);
-      } else {
-        const int wi = sl >> 2;
-        const uint32_t b = sl & 3;
-        h[m2] = bytes_to_halves<KV>(hi2[wi], lo[wi], pair_sel<KV>(b, b));
-      }
+    for (int e = 0; e < 8; ++e) {
+      float x = pr[8 * pp + e];
+      if constexpr (KV == PA_KV_INT8) x *= vsc[8 * pp + e];
+      pop[e] = (_Float16)x;
     }
-    const f16x8 vop = finish<KV>(as_f16x8(h[0], h[1], h[2], h[3]));
-    st.acc[sl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop, st.acc[sl], 0, 0, 0);
+#pragma unroll
+    for (int sl = 0; sl < G::kE; ++sl) {
+      uint32_t h[4];
+#pragma unroll
+      for (int m2 = 0; m2 < 4; ++m2) {
+        const uint32_t *lo = r.v[8 * pp + 2 * m2];
+        const uint32_t *hi2 = r.v[8 * pp + 2 * m2 + 1];
+        if constexpr (G::kElem == 2) {
+          const int wi = sl >> 1;
+          const uint32_t sel = (sl & 1) ? 0x07060302u : 0x05040100u;
+          h[m2] = perm(hi2[wi], lo[wi], sel);
+        } else {
+          const int wi = sl >> 2;
+          const uint32_t b = sl & 3;
+          h[m2] = bytes_to_halves<KV>(hi2[wi], lo[wi], pair_sel<KV>(b, b));
+        }
+      }
+      const f16x8 vop = finish<KV>(as_f16x8(h[0], h[1], h[2], h[3]));
+      st.acc[sl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop, st.acc[sl], 0, 0, 0);
+    }
   }
 }
 
@@ -447,13 +481,13 @@ struct SplitRange {
 
 __device__ __forceinline__ SplitRange split_range(int seq_len, int num_splits, int max_seq_len,
                                                   int split) {
-  const int64_t own = ((int64_t)seq_len + kTile - 1) / kTile;
+  const int64_t own = ((int64_t)seq_len + kSplitAlign - 1) / kSplitAlign;
   int64_t ntile_chunk = (own + num_splits - 1) / num_splits;
   if (max_seq_len > 0) {
-    const int64_t longest = ((int64_t)max_seq_len + kTile - 1) / kTile;
+    const int64_t longest = ((int64_t)max_seq_len + kSplitAlign - 1) / kSplitAlign;
     ntile_chunk = max((longest + num_splits - 1) / num_splits, ntile_chunk);
   }
-  const int64_t chunk = max(ntile_chunk, (int64_t)1) * kTile;  // T = 0 still has one split
+  const int64_t chunk = max(ntile_chunk, (int64_t)1) * kSplitAlign;  // T = 0 still has one split
   const int64_t lo = min((int64_t)split * chunk, (int64_t)seq_len);
   SplitRange r;
   r.lo = (int)lo;
@@ -487,7 +521,7 @@ paged_decode_kernel(const KParams p) {
   __shared__ __attribute__((aligned(16))) uint8_t sm_raw[kMergeBytes > kSlotsBytes ? kMergeBytes : kSlotsBytes];
   __shared__ float sm_m[kWaves][16];
   __shared__ float sm_l[kWaves][16];
-  __shared__ __attribute__((aligned(16))) float sm_sc[kWaves][64];
+  __shared__ __attribute__((aligned(16))) float sm_sc[kWaves][G::kScales];
   auto sm_acc = reinterpret_cast<float (*)[kRegs][64]>(sm_raw);
 
   const int lane = threadIdx.x & 63;
@@ -540,10 +574,10 @@ paged_decode_kernel(const KParams p) {
   const int32_t *bt_row = p.bt + (int64_t)b * p.sbtb;
   float *sc_lds = sm_sc[wave];
   uint8_t *k_lds = sm_raw + wave * G::kKSlotBytes;
-  const int ntiles = (hi > lo) ? (hi - lo + kTile - 1) / kTile : 0;
+  const int ntiles = (hi > lo) ? (hi - lo + G::kTT - 1) / G::kTT : 0;
   // this wave's tiles: wave + kWaves * i, i < cnt
   const int cnt = ntiles > wave ? (ntiles - wave + kWaves - 1) / kWaves : 0;
-  auto n0_of = [&](int i) { return lo + (wave + kWaves * i) * kTile; };
+  auto n0_of = [&](int i) { return lo + (wave + kWaves * i) * G::kTT; };
   if (cnt > 0) {
     if constexpr (G::kPrefetch) {
       Tile<KV, D> ta, tb;

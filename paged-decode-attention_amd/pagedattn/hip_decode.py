@@ -28,9 +28,11 @@ from .cache import PagedKVCache
 # workgroup, 32 tokens per wave iteration.
 WAVES_PER_WORKGROUP = 4
 TILE_TOKENS = 32
-# Workgroups of the decode kernel that fit on one CU at once at head_dim 128
-# (two 4-wave workgroups: 225 VGPR+AGPR per lane -> 2 waves per SIMD).
+# Workgroups of the decode kernel resident on one CU at head_dim 128 (two
+# 4-wave workgroups: the kernel is built for 2 waves per SIMD).
 RESIDENT_WORKGROUPS_PER_CU = 2
+# Smallest split chunk worth a workgroup (16 tiles, 4 per wave).
+MIN_SPLIT_TOKENS = 512
 
 _KV_CODE = {"fp16": _abi.PA_KV_FP16, "fp8_e5m2": _abi.PA_KV_FP8_E5M2, "int8": _abi.PA_KV_INT8}
 _STORE_DTYPE = {"fp16": torch.float16, "fp8_e5m2": torch.float8_e5m2, "int8": torch.int8}
@@ -42,20 +44,24 @@ def pick_num_splits(
 ) -> int:
     """Split count for the split-KV path, sized for the MI355X's 256 CUs.
 
-    Same signature as the reference (triton_decode.py:248-263), MI355X policy:
-    launch enough (batch, kv_head, split) workgroups to occupy every CU with
-    RESIDENT_WORKGROUPS_PER_CU workgroups, but never give a wave fewer than two
-    32-token tiles. No power-of-two rounding and no cap of 64, so a
-    long-context batch of 4 can use hundreds of splits. `block_n` is accepted
-    for signature compatibility.
+    Same signature as the reference (triton_decode.py:248-263), MI355X policy
+    from measurements of the BASELINE shapes:
+      * batch*kv_heads >= RESIDENT_WORKGROUPS_PER_CU * CUs (every CU already
+        holds its two resident workgroups): no split; a second pass costs
+        more than the balance it buys on uniform batches;
+      * otherwise enough splits for two rounds of resident workgroups
+        (4 per CU), but never chunks below MIN_SPLIT_TOKENS tokens; no
+        power-of-two rounding and no cap of 64, so a long-context batch of 4
+        uses dozens of splits.
+    `block_n` is accepted for signature compatibility.
     """
     del block_n
     base = max(1, batch * num_kv_heads)
-    target = RESIDENT_WORKGROUPS_PER_CU * max(1, sm_count)
-    if base >= target:
+    slots = RESIDENT_WORKGROUPS_PER_CU * max(1, sm_count)
+    if base >= slots:
         return 1
-    want = -(-target // base)
-    max_useful = max(1, max_seq_len // (2 * WAVES_PER_WORKGROUP * TILE_TOKENS))
+    want = -(-2 * slots // base)
+    max_useful = max(1, max_seq_len // MIN_SPLIT_TOKENS)
     return int(max(1, min(want, max_useful, _abi.PA_MAX_SPLITS)))
 
 
