@@ -12,6 +12,10 @@
  *                       (pagedattn/triton_decode.py:331-376)
  *   pa_split_reduce  <- `_split_reduce_kernel[(b, hq)](...)` on its own
  *                       (pagedattn/triton_decode.py:198-240, 368-376)
+ *   pa_cache_write   <- the KV write before the decode,
+ *                       `reshape_and_cache_flash` (integration/vllm_backend.py:
+ *                       117-122), with the reference's quantisation
+ *                       (pagedattn/cache.py:33-48)
  *
  * Everything is plain C: device pointers, sizes, element strides and enums.
  * No function throws; each returns PA_OK (0) or a negative PA_ERR_* code and
@@ -151,6 +155,40 @@ int pa_decode_partials(const pa_decode_args *args, void *stream);
  * sum_s 2^(lse_s - m), m = max_s lse_s; all-empty rows yield zeros.
  * Replaces pagedattn/triton_decode.py:198-240 / 368-376. */
 int pa_split_reduce(const pa_reduce_args *args, void *stream);
+
+/* Arguments of pa_cache_write: this step's K/V rows into the paged cache. */
+typedef struct pa_cache_write_args {
+  const void *key;   /* [num_tokens, num_kv_heads, head_dim] fp16, head_dim contiguous */
+  const void *value; /* same shape */
+  void *k_cache;     /* [num_blocks, block_size, num_kv_heads, head_dim] kv_dtype */
+  void *v_cache;     /* same shape and strides as k_cache */
+  void *k_scale;     /* [num_blocks, block_size, num_kv_heads] (int8 only; NULL otherwise) */
+  void *v_scale;     /* same shape and strides as k_scale */
+  const int64_t *slot_mapping; /* [num_tokens]: block * block_size + offset; < 0 skips */
+  int32_t num_tokens;
+  int32_t num_kv_heads;
+  int32_t head_dim;   /* 32, 64, 128 or 256 */
+  int32_t block_size; /* >= 1 */
+  int32_t num_blocks; /* slots at or past num_blocks * block_size are skipped */
+  int64_t stride_kt, stride_kh; /* key element strides (token, head) */
+  int64_t stride_vt, stride_vh; /* value element strides (token, head) */
+  int64_t stride_cn, stride_ct, stride_ch; /* cache element strides, shared by k/v */
+  int64_t stride_sn, stride_st;            /* scale element strides, shared by k/v */
+  int32_t kv_dtype;    /* PA_KV_* */
+  int32_t scale_dtype; /* PA_SCALE_* (int8: FP16 or FP32) */
+} pa_cache_write_args;
+
+/* Scatter this step's K and V rows (fp16) into the paged NHD cache at
+ * slot_mapping, quantising as the cache dtype requires, with the reference's
+ * semantics (pagedattn/cache.py:33-48): fp16 copies; fp8_e5m2 is the
+ * round-to-nearest-even cast (overflow to inf, as torch's); int8 takes one
+ * scale per (token, head): amax over head_dim clamped to 1e-6, scale =
+ * amax / 127 rounded to the scale type, q = round_half_even(x / scale)
+ * clamped to +-127, and writes the scale. Bit-identical to
+ * pagedattn.cache.quantize_kv. Replaces the call to vLLM's
+ * `reshape_and_cache_flash` at integration/vllm_backend.py:117-122 for
+ * caches in this library's formats. */
+int pa_cache_write(const pa_cache_write_args *args, void *stream);
 
 /* Message for the last non-zero return on the calling thread ("" if none). */
 const char *pa_last_error(void);

@@ -15,6 +15,9 @@ A from-scratch restatement, in torch on the CPU, of the reference's algorithm
                      :169-188 (normalised partial + log2-sum-exp, empty = -inf)
   split_merge        pagedattn/triton_decode.py:198-240
   sdpa_math_decode   pagedattn/reference.py:57-72 (SDPA math backend, GQA)
+  write_kv           the KV write before the decode (integration/vllm_backend.py:
+                     117-122, vLLM's reshape_and_cache_flash) with the
+                     quantisation of pagedattn/cache.py:33-48
 
 Deviations, each deliberate: `reference_decode` takes `sm_scale` (the
 reference always uses head_dim**-0.5, reference.py:45) and can return the
@@ -233,3 +236,22 @@ def bytes_read_per_decode_step(cache) -> int:
     if cache.kv_dtype == "int8":
         total += 2 * n_tok * h * cache.k_scale.element_size()
     return total
+
+
+def write_kv(key: torch.Tensor, value: torch.Tensor, cache, slot_mapping: torch.Tensor) -> None:
+    """Scatter key/value [n, H_kv, D] (fp16) into a CPU cache at slot_mapping,
+    row by row, quantised with `quantize_kv` (cache.py:33-48). Slots < 0 or at
+    or past num_blocks * block_size are skipped. Mutates `cache` in place."""
+    bs = cache.block_size
+    nb = cache.k_cache.shape[0]
+    slots = slot_mapping.cpu().long().tolist()
+    for t, slot in enumerate(slots):
+        if slot < 0 or slot >= nb * bs:
+            continue
+        blk, off = divmod(slot, bs)
+        for src, dst, dst_scale in ((key, cache.k_cache, cache.k_scale), (value, cache.v_cache, cache.v_scale)):
+            scale_dtype = dst_scale.dtype if dst_scale is not None else torch.float16
+            qv, s = quantize_kv(src[t].cpu().unsqueeze(0), cache.kv_dtype, scale_dtype)
+            dst[blk, off] = qv[0]
+            if s is not None:
+                dst_scale[blk, off] = s[0]

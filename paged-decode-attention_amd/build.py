@@ -13,7 +13,7 @@ import sys
 
 PKG_ROOT = pathlib.Path(__file__).resolve().parent
 REPO_ROOT = PKG_ROOT.parent
-SOURCES = [PKG_ROOT / "csrc" / "paged_decode.hip"]
+SOURCES = [PKG_ROOT / "csrc" / "paged_decode.hip", PKG_ROOT / "csrc" / "cache_write.hip"]
 OUTPUT = PKG_ROOT / "pagedattn" / "libpagedattn_hip.so"
 ARCH = os.environ.get("PAGEDATTN_ARCH", "gfx950")
 

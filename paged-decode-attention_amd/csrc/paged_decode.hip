@@ -50,6 +50,7 @@
 #include <string.h>
 
 #include "pagedattn.h"
+#include "pa_errors.h"
 
 namespace {
 
@@ -760,23 +761,19 @@ __global__ void __launch_bounds__(64) split_reduce_kernel(const RParams p) {
 // host side: validation, error reporting, dispatch
 // ----------------------------------------------------------------------------
 
-thread_local char g_err[512] = "";
-
 int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 int fail(int code, const char *fmt, ...) {
+  char msg[512];
   va_list ap;
   va_start(ap, fmt);
-  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  vsnprintf(msg, sizeof(msg), fmt, ap);
   va_end(ap);
-  return code;
+  return pa_fail(code, "%s", msg);
 }
 
-int ok() {
-  g_err[0] = '\0';
-  return PA_OK;
-}
+int ok() { return pa_ok(); }
 
-bool aligned(const void *ptr, int a) { return (reinterpret_cast<uintptr_t>(ptr) % a) == 0; }
+bool aligned(const void *ptr, int a) { return pa_aligned(ptr, a); }
 
 bool is_pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
 
@@ -998,6 +995,25 @@ pa_reduce_args reduce_args_from(const pa_decode_args *a) {
 }
 
 }  // namespace
+
+namespace {
+thread_local char g_err[512] = "";
+}  // namespace
+
+int pa_fail(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int pa_ok() {
+  g_err[0] = '\0';
+  return PA_OK;
+}
+
+const char *pa_error_message() { return g_err; }
 
 extern "C" {
 

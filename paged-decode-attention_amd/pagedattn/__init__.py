@@ -9,6 +9,7 @@ the package (oracle/).
 
 from .config import LLAMA3_8B, LLAMA3_70B, MHA_DEBUG, QWEN25_05B, KVDType, ModelShape, kv_bytes_per_token
 from .cache import PagedKVCache, allocate, quantize_kv
+from .cache_ops import reshape_and_cache
 from .hip_decode import (
     decode_partials,
     paged_decode_hip,
@@ -20,7 +21,7 @@ from .hip_decode import (
 __all__ = [
     "LLAMA3_8B", "LLAMA3_70B", "MHA_DEBUG", "QWEN25_05B", "KVDType", "ModelShape",
     "kv_bytes_per_token",
-    "PagedKVCache", "allocate", "quantize_kv",
+    "PagedKVCache", "allocate", "quantize_kv", "reshape_and_cache",
     "paged_decode_hip", "paged_decode_triton", "pick_num_splits",
     "decode_partials", "split_reduce",
 ]

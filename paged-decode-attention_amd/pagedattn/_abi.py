@@ -39,6 +39,7 @@ EXPORTED_SYMBOLS = (
     "pa_decode",
     "pa_decode_partials",
     "pa_split_reduce",
+    "pa_cache_write",
     "pa_last_error",
     "pa_abi_version",
 )
@@ -111,6 +112,34 @@ class PaReduceArgs(ctypes.Structure):
     ]
 
 
+class PaCacheWriteArgs(ctypes.Structure):
+    _fields_ = [
+        ("key", _vp),
+        ("value", _vp),
+        ("k_cache", _vp),
+        ("v_cache", _vp),
+        ("k_scale", _vp),
+        ("v_scale", _vp),
+        ("slot_mapping", _vp),
+        ("num_tokens", _i32),
+        ("num_kv_heads", _i32),
+        ("head_dim", _i32),
+        ("block_size", _i32),
+        ("num_blocks", _i32),
+        ("stride_kt", _i64),
+        ("stride_kh", _i64),
+        ("stride_vt", _i64),
+        ("stride_vh", _i64),
+        ("stride_cn", _i64),
+        ("stride_ct", _i64),
+        ("stride_ch", _i64),
+        ("stride_sn", _i64),
+        ("stride_st", _i64),
+        ("kv_dtype", _i32),
+        ("scale_dtype", _i32),
+    ]
+
+
 class HipLibraryMissing(ImportError):
     """The HIP library has not been built (run __graft_entry__.build())."""
 
@@ -147,6 +176,8 @@ def load() -> ctypes.CDLL:
         lib.pa_decode_partials.restype = ctypes.c_int
         lib.pa_split_reduce.argtypes = [ctypes.POINTER(PaReduceArgs), _vp]
         lib.pa_split_reduce.restype = ctypes.c_int
+        lib.pa_cache_write.argtypes = [ctypes.POINTER(PaCacheWriteArgs), _vp]
+        lib.pa_cache_write.restype = ctypes.c_int
         lib.pa_last_error.argtypes = []
         lib.pa_last_error.restype = ctypes.c_char_p
         lib.pa_abi_version.argtypes = []

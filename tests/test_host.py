@@ -51,10 +51,14 @@ def test_library_exports_every_declared_symbol():
     assert lib.pa_abi_version() == _abi.PA_ABI_VERSION
 
 
+STRUCTS = (("pa_decode_args", _abi.PaDecodeArgs), ("pa_reduce_args", _abi.PaReduceArgs),
+           ("pa_cache_write_args", _abi.PaCacheWriteArgs))
+
+
 def test_struct_layout_matches_header(tmp_path):
     """ctypes mirrors of pa_decode_args / pa_reduce_args against gcc's layout."""
     lines = ['#include <stddef.h>', '#include <stdio.h>', '#include "pagedattn.h"', 'int main(void){']
-    for cname, cls in (("pa_decode_args", _abi.PaDecodeArgs), ("pa_reduce_args", _abi.PaReduceArgs)):
+    for cname, cls in STRUCTS:
         lines.append(f'printf("{cname} sizeof %zu\\n", sizeof({cname}));')
         for f, _ in cls._fields_:
             lines.append(f'printf("{cname} {f} %zu\\n", offsetof({cname}, {f}));')
@@ -68,7 +72,7 @@ def test_struct_layout_matches_header(tmp_path):
     for line in filter(None, got):
         s, f, v = line.split()
         table[(s, f)] = int(v)
-    for cname, cls in (("pa_decode_args", _abi.PaDecodeArgs), ("pa_reduce_args", _abi.PaReduceArgs)):
+    for cname, cls in STRUCTS:
         assert table[(cname, "sizeof")] == ctypes.sizeof(cls)
         for f, _ in cls._fields_:
             assert table[(cname, f)] == getattr(cls, f).offset, (cname, f)
@@ -160,6 +164,58 @@ def test_null_args_and_reduce_validation():
     assert lib.pa_split_reduce(ctypes.byref(r), None) == _abi.PA_ERR_INVALID
     r.num_splits, r.stride_ob = 2, -1
     assert lib.pa_split_reduce(ctypes.byref(r), None) == _abi.PA_ERR_INVALID
+
+
+def _write_args(**over):
+    a = _abi.PaCacheWriteArgs()
+    a.key = a.value = a.k_cache = a.v_cache = a.slot_mapping = FAKE
+    a.num_tokens, a.num_kv_heads, a.head_dim, a.block_size, a.num_blocks = 4, 8, 128, 16, 32
+    a.stride_kt, a.stride_kh, a.stride_vt, a.stride_vh = 1024, 128, 1024, 128
+    a.stride_cn, a.stride_ct, a.stride_ch = 16 * 1024, 1024, 128
+    a.kv_dtype, a.scale_dtype = _abi.PA_KV_FP16, _abi.PA_SCALE_NONE
+    for k, v in over.items():
+        setattr(a, k, v)
+    return a
+
+
+WRITE_INVALID = [
+    ("key", dict(key=None), _abi.PA_ERR_INVALID),
+    ("tokens", dict(num_tokens=-1), _abi.PA_ERR_INVALID),
+    ("heads", dict(num_kv_heads=0), _abi.PA_ERR_INVALID),
+    ("head_dim", dict(head_dim=80), _abi.PA_ERR_UNSUPPORTED),
+    ("kv_dtype", dict(kv_dtype=5), _abi.PA_ERR_INVALID),
+    ("int8_scales", dict(kv_dtype=_abi.PA_KV_INT8, scale_dtype=_abi.PA_SCALE_FP32), _abi.PA_ERR_INVALID),
+    ("scale_on_fp16", dict(scale_dtype=_abi.PA_SCALE_FP16), _abi.PA_ERR_INVALID),
+    ("misaligned_key", dict(key=FAKE + 8), _abi.PA_ERR_INVALID),
+    ("misaligned_cache", dict(stride_ch=100), _abi.PA_ERR_INVALID),
+    ("negative_stride", dict(stride_vt=-1), _abi.PA_ERR_INVALID),
+]
+
+
+@cpu_only
+@pytest.mark.parametrize("name,over,code", WRITE_INVALID, ids=[c[0] for c in WRITE_INVALID])
+def test_pa_cache_write_rejects(name, over, code):
+    lib = _lib()
+    a = _write_args(**over)
+    assert lib.pa_cache_write(ctypes.byref(a), None) == code
+    assert lib.pa_last_error().decode()
+
+
+@cpu_only
+def test_pa_cache_write_null_and_empty():
+    lib = _lib()
+    assert lib.pa_cache_write(None, None) == _abi.PA_ERR_INVALID
+    # zero tokens is a no-op that returns before any HIP call
+    assert lib.pa_cache_write(ctypes.byref(_write_args(num_tokens=0)), None) == _abi.PA_OK
+
+
+def test_cache_writer_rejects_cpu_tensors():
+    from pagedattn import reshape_and_cache
+
+    c = allocate(LLAMA3_8B, 1, [16], device="cpu", seed=0)
+    k = torch.zeros((2, 8, 128), dtype=torch.float16)
+    with pytest.raises(ValueError, match="GPU"):
+        reshape_and_cache(k, k, c, torch.zeros(2, dtype=torch.int64))
 
 
 def test_python_errors_from_codes():

@@ -449,3 +449,57 @@ def test_planted_dequant_mistake_is_caught():
                                    "v_scale": torch.ones_like(c.v_scale)})
     got_bad = oracle.reference_decode(q, bad, out_dtype=torch.float32)
     assert (got_bad.double() - c_oracle.decode(q, c)).abs().max().item() > 1e-1
+
+
+# --------------------------------------------------------------------------
+# the KV write (vllm_backend.py:117-122 with cache.py:33-48 quantisation)
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("kv_dtype,scale_dtype", [("fp16", torch.float16), ("fp8_e5m2", torch.float16),
+                                                  ("int8", torch.float16), ("int8", torch.float32)])
+def test_write_kv_equals_quantize(kv_dtype, scale_dtype):
+    """Writing rows one slot at a time stores exactly quantize_kv of the rows,
+    skips negative and out-of-pool slots, and leaves other slots untouched."""
+    c = _cache(LLAMA3_8B, [40], kv_dtype, seed=21, scale_dtype=scale_dtype, slack=2)
+    before_k = c.k_cache.clone()
+    g = torch.Generator().manual_seed(22)
+    n = 6
+    key = torch.randn((n, 8, 128), generator=g).half() * 3
+    value = torch.randn((n, 8, 128), generator=g).half()
+    nb = c.k_cache.shape[0]
+    slots = torch.tensor([5, -1, 17, nb * 16 + 3, 0, 47], dtype=torch.int64)
+    oracle.write_kv(key, value, c, slots)
+    qk, sk = oracle.quantize_kv(key, kv_dtype, scale_dtype)
+    qv, sv = oracle.quantize_kv(value, kv_dtype, scale_dtype)
+    raw = lambda t: t.view(torch.uint8) if t.element_size() == 1 else t
+    for t, slot in enumerate(slots.tolist()):
+        if slot < 0 or slot >= nb * 16:
+            continue
+        blk, off = divmod(slot, 16)
+        assert torch.equal(raw(c.k_cache[blk, off]), raw(qk[t]))
+        assert torch.equal(raw(c.v_cache[blk, off]), raw(qv[t]))
+        if sk is not None:
+            assert torch.equal(c.k_scale[blk, off], sk[t]) and torch.equal(c.v_scale[blk, off], sv[t])
+    untouched = [s for s in range(nb * 16) if s not in slots.tolist()]
+    for slot in untouched[:50]:
+        blk, off = divmod(slot, 16)
+        assert torch.equal(raw(c.k_cache[blk, off]), raw(before_k[blk, off]))
+
+
+def test_write_then_decode_reads_the_new_token():
+    """A token written at position T of a sequence is attended by the next
+    decode: the dominant-logit closed form on the written key."""
+    c = _cache(ModelShape(8, 2, 64, "w"), [31], "fp16", seed=23, slack=1)
+    bt = c.block_table
+    T = 31
+    slot = int(bt[0, T // 16]) * 16 + T % 16
+    q = torch.zeros((1, 8, 64), dtype=torch.float16)
+    q[:, :, 0] = 1.0
+    key = torch.zeros((1, 2, 64), dtype=torch.float16)
+    key[0, :, 0] = 400.0
+    value = torch.randn((1, 2, 64), generator=torch.Generator().manual_seed(24)).half()
+    oracle.write_kv(key, value, c, torch.tensor([slot]))
+    c.seq_lens = torch.tensor([T + 1], dtype=torch.int32)
+    out = oracle.reference_decode(q, c, out_dtype=torch.float32)
+    for h in range(8):
+        assert (out[0, h] - value[0, h // 4].float()).abs().max().item() < 1e-3
