@@ -170,6 +170,63 @@ def _algorithmic_bytes(cache) -> int:
     return kv + 2 * b * s.num_q_heads * s.head_dim * 2 + 4 * pages
 
 
+def bench_write(args, wl, shape, cache, dev) -> int:
+    """The KV-cache write (pa_cache_write) of --write-tokens fp16 K/V rows into
+    random slots of the workload's pool, in the workload's KV dtype; checked
+    bit-exact against the oracle on a sample first."""
+    import torch
+
+    from oracle import reference as oracle
+    from pagedattn import reshape_and_cache
+
+    n = min(args.write_tokens, cache.k_cache.shape[0] * cache.block_size)
+    g = torch.Generator().manual_seed(7)
+    h, d = shape.num_kv_heads, shape.head_dim
+    key = torch.randn((n, h, d), generator=g, dtype=torch.float16).to(dev)
+    value = torch.randn((n, h, d), generator=g, dtype=torch.float16).to(dev)
+    slots = torch.randperm(cache.k_cache.shape[0] * cache.block_size, generator=g)[:n].to(dev)
+    # parity on a 64-row sample
+    sample = slots[:64].cpu()
+    reshape_and_cache(key[:64], value[:64], cache, slots[:64])
+    torch.cuda.synchronize()
+    blk, off = sample // cache.block_size, sample % cache.block_size
+    want_k, want_ks = oracle.quantize_kv(key[:64].cpu(), cache.kv_dtype,
+                                         cache.k_scale.dtype if cache.k_scale is not None else torch.float16)
+    got_k = cache.k_cache[blk.to(dev), off.to(dev)].cpu()
+    raw = lambda t: t.view(torch.uint8) if t.element_size() == 1 else t
+    exact = bool(torch.equal(raw(got_k), raw(want_k)))
+    if want_ks is not None:
+        exact = exact and bool(torch.equal(cache.k_scale[blk.to(dev), off.to(dev)].cpu(), want_ks))
+    _log(f"write parity on 64 rows: bit-exact={exact}")
+    if not exact:
+        return 1
+    for _ in range(args.warmup):
+        reshape_and_cache(key, value, cache, slots)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(args.steps):
+        reshape_and_cache(key, value, cache, slots)
+    ev1.record()
+    torch.cuda.synchronize()
+    us = ev0.elapsed_time(ev1) / args.steps * 1e3
+    elem = cache.k_cache.element_size()
+    sbytes = 0 if cache.k_scale is None else cache.k_scale.element_size()
+    algo = n * h * d * 2 * 2 + n * h * d * elem * 2 + n * 8 + n * h * sbytes * 2
+    gbs = algo / (us * 1e-6) / 1e9
+    print(json.dumps({
+        "metric": "kv cache write GB/s", "value": round(gbs, 2), "unit": "GB/s",
+        "us_per_call": round(us, 2), "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "higher_is_better": True, "dtype": cache.kv_dtype, "data": "synthetic",
+        "config": {"workload": f"{wl.name} pool, {n} rows [{h}, {d}] fp16 -> {cache.kv_dtype}"},
+        "algorithmic_bytes_per_call": algo, "parity_bit_exact": exact,
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "cache_write_kernel",
+                     "kernel_us": round(us, 2)},
+    }), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -182,6 +239,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 1 GiB device copy (PMC calibration of FETCH/WRITE_SIZE)")
+    ap.add_argument("--op", default="decode", choices=["decode", "write"],
+                    help="decode (the headline) or write: the KV-cache write of --write-tokens rows")
+    ap.add_argument("--write-tokens", type=int, default=65536)
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -220,6 +280,9 @@ def main() -> int:
             v_scale=None if cache.v_scale is None else cache.v_scale.clone()))
     torch.cuda.synchronize()
     _log(f"allocated {copies} pool copies of {pool_bytes / 2**30:.2f} GiB in {time.perf_counter() - t0:.1f} s")
+
+    if args.op == "write":
+        return bench_write(args, wl, shape, cache, dev)
 
     cus = _cu_count(dev)
     splits = args.splits or pick_num_splits(wl.batch, shape.num_kv_heads, max(wl.lens), cus)

@@ -86,13 +86,34 @@ def _reason_to_delegate(impl, attn_metadata, kv_cache, output, output_scale) -> 
     return ""
 
 
+def _vllm_cache_op():
+    """vLLM's `reshape_and_cache_flash`, or None where vLLM's ops are absent."""
+    try:
+        return torch.ops._C_cache_ops.reshape_and_cache_flash
+    except (AttributeError, RuntimeError):
+        return None
+
+
 def _write_kv(layer, impl, key, value, key_cache, value_cache, slot_mapping) -> None:
-    """This step's K/V into the paged cache, with vLLM's own op
-    (`reshape_and_cache_flash`, vllm_backend.py:117-122)."""
-    torch.ops._C_cache_ops.reshape_and_cache_flash(
-        key, value, key_cache, value_cache, slot_mapping, impl.kv_cache_dtype,
-        layer._k_scale, layer._v_scale,
-    )
+    """This step's K/V into the paged cache (vllm_backend.py:117-122).
+
+    vLLM's own op when it is loaded; otherwise this library's HIP writer,
+    which stores the same bytes for the fp16 caches this backend serves
+    (`_reason_to_delegate` sends every other cache dtype to vLLM).
+    """
+    op = _vllm_cache_op()
+    if op is not None:
+        op(key, value, key_cache, value_cache, slot_mapping, impl.kv_cache_dtype,
+           layer._k_scale, layer._v_scale)
+        return
+    from pagedattn.cache_ops import reshape_and_cache
+
+    n = int(slot_mapping.shape[0])
+    view = PagedKVCache(
+        shape=ModelShape(impl.num_heads, impl.num_kv_heads, impl.head_size, name="vllm"),
+        block_size=int(key_cache.shape[1]), kv_dtype="fp16", k_cache=key_cache,
+        v_cache=value_cache, k_scale=None, v_scale=None, block_table=None, seq_lens=None)
+    reshape_and_cache(key[:n], value[:n], view, slot_mapping.to(torch.int64))
 
 
 _CU_COUNT: dict[int, int] = {}

@@ -30,6 +30,50 @@ class _BaseImpl:
         raise AssertionError("decode must not be delegated")
 
 
+def test_impl_forward_writes_the_step_kv():
+    """The full decode step through the boundary: this step's K/V are written
+    (vLLM's op is absent here, so the HIP writer does it) and attended."""
+    _, Impl = vb.build_backend_classes(object, _BaseImpl)
+    shape = LLAMA3_8B
+    lens = [16, 40, 1]  # lengths before this step
+    n = len(lens)
+    c = allocate(shape, n, lens, seed=32, device="cuda", slack_blocks=6)
+    bt = c.block_table.clone()
+    if bt.shape[1] < 4:
+        bt = torch.cat([bt, torch.zeros((n, 4 - bt.shape[1]), dtype=torch.int32, device="cuda")], 1)
+    used = {int(bt[b, j]) for b, t in enumerate(lens) for j in range(-(-t // 16))}
+    free = [i for i in range(c.k_cache.shape[0]) if i not in used]
+    slots = []
+    for b, t in enumerate(lens):
+        if t % 16 == 0:
+            bt[b, t // 16] = free.pop()
+        slots.append(int(bt[b, t // 16]) * 16 + t % 16)
+    kv_cache = torch.stack([c.k_cache, c.v_cache])
+    g = torch.Generator().manual_seed(33)
+    key = torch.randn((n, shape.num_kv_heads, shape.head_dim), generator=g).half().cuda()
+    value = torch.randn((n, shape.num_kv_heads, shape.head_dim), generator=g).half().cuda()
+    new_lens = torch.tensor([t + 1 for t in lens], dtype=torch.int32, device="cuda")
+    meta = types.SimpleNamespace(max_query_len=1, num_actual_tokens=n, use_cascade=False,
+                                 local_attn_metadata=None, max_seq_len=max(lens) + 1,
+                                 block_table=bt, seq_lens=new_lens,
+                                 slot_mapping=torch.tensor(slots, dtype=torch.int64, device="cuda"))
+    query = seeded_q(n, shape.num_q_heads, shape.head_dim, 33, device="cuda")
+    output = torch.zeros_like(query)
+    impl = Impl(shape)
+    impl.kv_sharing_target_layer_name = None  # this layer writes its own K/V
+    layer = types.SimpleNamespace(_k_scale=None, _v_scale=None)
+    impl.forward(layer, query, key, value, kv_cache, meta, output)
+    torch.cuda.synchronize()
+    # oracle: the same cache with the new rows written on the CPU
+    import dataclasses
+    ref = dataclasses.replace(c, k_cache=c.k_cache.cpu().clone(), v_cache=c.v_cache.cpu().clone(),
+                              block_table=bt.cpu(), seq_lens=new_lens.cpu())
+    oracle.write_kv(key.cpu(), value.cpu(), ref, torch.tensor(slots))
+    assert torch.equal(kv_cache[0].cpu(), ref.k_cache) and torch.equal(kv_cache[1].cpu(), ref.v_cache)
+    want = oracle.reference_decode(query, ref, out_dtype=torch.float32)
+    assert max_abs(output, want) < 2e-3
+
+
 @pytest.mark.parametrize("shape,lens", [(LLAMA3_8B, [300, 1, 4096]), (QWEN25_05B, [32, 192, 77, 5])])
 def test_impl_forward_matches_oracle(shape, lens):
     _, Impl = vb.build_backend_classes(object, _BaseImpl)
