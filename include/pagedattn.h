@@ -27,12 +27,12 @@
  * including the split-KV workspace (part_out / part_lse).
  *
  * Tensor layouts (element strides; the innermost dimension is contiguous):
- *   q          [batch, num_q_heads, head_dim]                  fp16
- *   k_cache    [num_blocks, block_size, num_kv_heads, head_dim] fp16 | fp8_e5m2 | int8
+ *   q          [batch, num_q_heads, head_dim]                  fp16 | bf16
+ *   k_cache    [num_blocks, block_size, num_kv_heads, head_dim] fp16 | fp8_e5m2 | int8 | bf16
  *   v_cache    same shape and strides as k_cache
  *   k_scale    [num_blocks, block_size, num_kv_heads]           fp16 | fp32 (int8 only)
  *   v_scale    same shape and strides as k_scale
- *   out        [batch, num_q_heads, head_dim]                  fp16
+ *   out        [batch, num_q_heads, head_dim]                  fp16 | bf16 (= q's)
  *   part_out   [batch, num_q_heads, num_splits, head_dim]      fp32
  *   part_lse   [batch, num_q_heads, num_splits]                fp32, log2 domain
  *   block_table[batch, max_blocks]                             int32
@@ -60,14 +60,21 @@ extern "C" {
 #define PA_KV_FP16 0
 #define PA_KV_FP8_E5M2 1 /* OCP e5m2 (torch.float8_e5m2), not the FNUZ variant */
 #define PA_KV_INT8 2
+/* bf16 rows, converted in registers to fp16 (round to nearest even) before
+ * the fp16 arithmetic: the reference maps bf16 to its fp16 path
+ * (`_KV_CODE["bf16"] = 0`, `k.to(tl.float16)`, pagedattn/triton_decode.py:30,
+ * 151-153; dequantize_kv, pagedattn/cache.py:55-56). */
+#define PA_KV_BF16 3
 
 /* Per-(token, kv_head) dequantization scale type (int8 KV only). */
 #define PA_SCALE_NONE 0
 #define PA_SCALE_FP16 1 /* the reference's choice (pagedattn/cache.py:45) */
 #define PA_SCALE_FP32 2
 
-/* q / out element type. */
+/* q / out element type. bf16 q is converted to fp16 (exact for normal
+ * values), bf16 out is rounded to nearest even from fp32. */
 #define PA_IO_FP16 0
+#define PA_IO_BF16 1
 
 /* Largest supported split count and GQA group handled in one pass. */
 #define PA_MAX_SPLITS 4096
@@ -158,7 +165,7 @@ int pa_split_reduce(const pa_reduce_args *args, void *stream);
 
 /* Arguments of pa_cache_write: this step's K/V rows into the paged cache. */
 typedef struct pa_cache_write_args {
-  const void *key;   /* [num_tokens, num_kv_heads, head_dim] fp16, head_dim contiguous */
+  const void *key;   /* [num_tokens, num_kv_heads, head_dim] fp16 (bf16 for a bf16 cache), head_dim contiguous */
   const void *value; /* same shape */
   void *k_cache;     /* [num_blocks, block_size, num_kv_heads, head_dim] kv_dtype */
   void *v_cache;     /* same shape and strides as k_cache */

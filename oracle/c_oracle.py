@@ -15,7 +15,7 @@ import torch
 
 from . import C_LIBRARY, build_c_oracle
 
-_KV = {"fp16": 0, "fp8_e5m2": 1, "int8": 2}
+_KV = {"fp16": 0, "fp8_e5m2": 1, "int8": 2, "bf16": 3}
 _SC = {None: 0, torch.float16: 1, torch.float32: 2}
 _LIB = None
 

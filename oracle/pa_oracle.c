@@ -10,7 +10,8 @@
  * double precision throughout.
  *
  *   dequant            pagedattn/cache.py:51-62  (e5m2 -> fp16 exact; int8 ->
- *                      fp16(int8 * scale), product formed in the scale's type)
+ *                      fp16(int8 * scale), product formed in the scale's type;
+ *                      bf16 -> fp16 rounded to nearest even)
  *   pa_oracle_decode   pagedattn/reference.py:28-49 (softmax(q.K^T * scale) V
  *                      over positions [0, seq_len), kv head = q head / group)
  *   pa_oracle_split    pagedattn/triton_decode.py:78-85 (split ranges) and
@@ -28,7 +29,7 @@
 #include <stdlib.h>
 #include <string.h>
 
-enum { KV_FP16 = 0, KV_FP8_E5M2 = 1, KV_INT8 = 2 };
+enum { KV_FP16 = 0, KV_FP8_E5M2 = 1, KV_INT8 = 2, KV_BF16 = 3 };
 enum { SC_NONE = 0, SC_FP16 = 1, SC_FP32 = 2 };
 
 /* IEEE binary16: 1 sign, 5 exponent (bias 15), 10 mantissa bits. */
@@ -99,6 +100,16 @@ static void load_row(const cache_t *c, const uint8_t *base, const uint8_t *sbase
       uint16_t h;
       memcpy(&h, p + 2 * i, 2);
       dst[i] = pa_oracle_half_to_double(h);
+    }
+  } else if (c->kv_dtype == KV_BF16) {
+    const uint8_t *p = base + row * c->d * 2;
+    for (int i = 0; i < c->d; ++i) {
+      uint16_t h;
+      memcpy(&h, p + 2 * i, 2);
+      const uint32_t u = (uint32_t)h << 16;
+      float f;
+      memcpy(&f, &u, 4);
+      dst[i] = pa_oracle_round_half((double)f);
     }
   } else if (c->kv_dtype == KV_FP8_E5M2) {
     const uint8_t *p = base + row * c->d;

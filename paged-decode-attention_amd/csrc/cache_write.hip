@@ -5,7 +5,7 @@
 // path (`reshape_and_cache_flash`, integration/vllm_backend.py:117-122) for
 // caches in this library's formats, with the quantisation semantics of
 // pagedattn/cache.py:33-48:
-//   fp16      copy
+//   fp16      copy (bf16 rows into a bf16 cache: copy too)
 //   fp8_e5m2  round-to-nearest-even of the fp16 bit pattern to its high byte
 //             (e5m2 shares fp16's exponent); overflow rounds to inf and NaN
 //             stays NaN, as torch's cast does
@@ -84,7 +84,7 @@ __global__ void __launch_bounds__(256) cache_write_kernel(const WParams p) {
       hv[2 * i] = w[i] & 0xffffu;
       hv[2 * i + 1] = w[i] >> 16;
     }
-    if constexpr (KV == PA_KV_FP16) {
+    if constexpr (KV == PA_KV_FP16 || KV == PA_KV_BF16) {
       if (live) *reinterpret_cast<u32x4 *>(dst + cbase + piece * 16) = w;
     } else if constexpr (KV == PA_KV_FP8_E5M2) {
       uint32_t b[8];
@@ -156,13 +156,14 @@ extern "C" int pa_cache_write(const pa_cache_write_args *a, void *stream) {
                    a->num_kv_heads, a->block_size, a->num_blocks);
   if (a->head_dim != 32 && a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256)
     return pa_fail(PA_ERR_UNSUPPORTED, "head_dim %d not in (32, 64, 128, 256)", a->head_dim);
-  if (a->kv_dtype != PA_KV_FP16 && a->kv_dtype != PA_KV_FP8_E5M2 && a->kv_dtype != PA_KV_INT8)
+  if (a->kv_dtype != PA_KV_FP16 && a->kv_dtype != PA_KV_FP8_E5M2 && a->kv_dtype != PA_KV_INT8 &&
+      a->kv_dtype != PA_KV_BF16)
     return pa_fail(PA_ERR_INVALID, "kv_dtype %d unknown", a->kv_dtype);
   const int64_t strides[] = {a->stride_kt, a->stride_kh, a->stride_vt, a->stride_vh,
                              a->stride_cn, a->stride_ct, a->stride_ch};
   for (int64_t s : strides)
     if (s < 0) return pa_fail(PA_ERR_INVALID, "strides must be non-negative");
-  const int elem = a->kv_dtype == PA_KV_FP16 ? 2 : 1;
+  const int elem = (a->kv_dtype == PA_KV_FP16 || a->kv_dtype == PA_KV_BF16) ? 2 : 1;
   const int piece = 8 * elem;  // bytes a lane stores
   if (!pa_aligned(a->key, 16) || !pa_aligned(a->value, 16) || (a->stride_kt * 2) % 16 ||
       (a->stride_kh * 2) % 16 || (a->stride_vt * 2) % 16 || (a->stride_vh * 2) % 16)
@@ -213,6 +214,7 @@ extern "C" int pa_cache_write(const pa_cache_write_args *a, void *stream) {
   const int d = a->head_dim;
   hipError_t e;
   if (a->kv_dtype == PA_KV_FP16) e = launch_w<PA_KV_FP16, PA_SCALE_NONE>(p, d, (int)grid, st);
+  else if (a->kv_dtype == PA_KV_BF16) e = launch_w<PA_KV_BF16, PA_SCALE_NONE>(p, d, (int)grid, st);
   else if (a->kv_dtype == PA_KV_FP8_E5M2) e = launch_w<PA_KV_FP8_E5M2, PA_SCALE_NONE>(p, d, (int)grid, st);
   else if (a->scale_dtype == PA_SCALE_FP32) e = launch_w<PA_KV_INT8, PA_SCALE_FP32>(p, d, (int)grid, st);
   else e = launch_w<PA_KV_INT8, PA_SCALE_FP16>(p, d, (int)grid, st);

@@ -86,12 +86,14 @@ struct KParams {
   int64_t slb, slh;          // elements
   int64_t sbtb;              // elements
   float qk_scale;            // sm_scale * log2(e)
+  int32_t io_bf16;           // q and out are bf16 (else fp16)
 };
 
 struct RParams {
   const float *part_out;
   const float *part_lse;
   uint8_t *out;
+  int32_t io_bf16;  // out is bf16 (else fp16)
   const int32_t *seq_lens;  // AUTO merge only
   int32_t max_tokens, max_seq_len;  // AUTO merge only
   int32_t num_heads, num_splits;
@@ -129,6 +131,38 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
 __device__ __forceinline__ f16x8 as_f16x8(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
   u32x4 u = {w0, w1, w2, w3};
   return __builtin_bit_cast(f16x8, u);
+}
+
+// Two bf16 values (one dword) -> two fp16, each rounded to nearest even.
+__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w) {
+  const f16x2 h = {(_Float16)__uint_as_float(w << 16), (_Float16)__uint_as_float(w & 0xffff0000u)};
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+__device__ __forceinline__ f16x8 bf16x8_to_f16x8(u32x4 w) {
+  return as_f16x8(bf16x2_to_f16x2(w.x), bf16x2_to_f16x2(w.y), bf16x2_to_f16x2(w.z),
+                  bf16x2_to_f16x2(w.w));
+}
+
+// fp32 -> bf16 bits, round to nearest even (NaN stays NaN).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+// Store n (a multiple of 4, or 2) fp32 values to an fp16 or bf16 row.
+__device__ __forceinline__ void store_row(uint8_t *dst, const float *y, int n, bool bf16) {
+  for (int e = 0; e + 1 < n; e += 2) {
+    uint32_t w;
+    if (bf16) {
+      w = f32_to_bf16_bits(y[e]) | (f32_to_bf16_bits(y[e + 1]) << 16);
+    } else {
+      const f16x2 h = {(_Float16)y[e], (_Float16)y[e + 1]};
+      w = __builtin_bit_cast(uint32_t, h);
+    }
+    reinterpret_cast<uint32_t *>(dst)[e / 2] = w;
+  }
 }
 
 // int8 operands hold 1152 + x; remove the offset (exact in fp16).
@@ -211,7 +245,7 @@ __device__ __forceinline__ float load_scale(const uint8_t *p) {
 // for k-step ks. Q uses the same mapping, which is all the reduction needs.
 template <int KV, int D>
 struct Geo {
-  static constexpr int kElem = (KV == PA_KV_FP16) ? 2 : 1;  // stored bytes/elem
+  static constexpr int kElem = (KV == PA_KV_FP16 || KV == PA_KV_BF16) ? 2 : 1;  // stored bytes/elem
   static constexpr int kKSteps = D / 32;                    // QK MFMAs per sub-tile
   static constexpr int kE = D / 16;                         // V elems per lane row
   static constexpr int kVBytes = kE * kElem;                // V bytes per lane row
@@ -380,7 +414,9 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
     for (int ks = 0; ks < G::kKSteps; ++ks) {
       f16x8 kop;
       const uint8_t *src = k_lds + (16 * u + r16) * G::kKSlotStride + (32 * ks + 8 * c) * G::kElem;
-      if constexpr (G::kElem == 2) {
+      if constexpr (KV == PA_KV_BF16) {
+        kop = bf16x8_to_f16x8(*reinterpret_cast<const u32x4 *>(src));
+      } else if constexpr (G::kElem == 2) {
         kop = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4 *>(src));
       } else {
         const u32x2 w = *reinterpret_cast<const u32x2 *>(src);
@@ -458,6 +494,7 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
           const int wi = sl >> 1;
           const uint32_t sel = (sl & 1) ? 0x07060302u : 0x05040100u;
           h[m2] = perm(hi2[wi], lo[wi], sel);
+          if constexpr (KV == PA_KV_BF16) h[m2] = bf16x2_to_f16x2(h[m2]);
         } else {
           const int wi = sl >> 2;
           const uint32_t b = sl & 3;
@@ -562,12 +599,15 @@ paged_decode_kernel(const KParams p) {
   for (int sl = 0; sl < G::kE; ++sl) st.acc[sl] = f32x4{0.f, 0.f, 0.f, 0.f};
   {
     const bool hv = r16 < nh;
-    const _Float16 *qrow = reinterpret_cast<const _Float16 *>(p.q) + (int64_t)b * p.sqb +
+    const uint16_t *qrow = reinterpret_cast<const uint16_t *>(p.q) + (int64_t)b * p.sqb +
                            (int64_t)(qh0 + (hv ? r16 : 0)) * p.sqh;
 #pragma unroll
     for (int ks = 0; ks < G::kKSteps; ++ks) {
       f16x8 qv = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (hv) qv = *reinterpret_cast<const f16x8 *>(qrow + 32 * ks + 8 * c);
+      if (hv) {
+        const u32x4 w = *reinterpret_cast<const u32x4 *>(qrow + 32 * ks + 8 * c);
+        qv = p.io_bf16 ? bf16x8_to_f16x8(w) : __builtin_bit_cast(f16x8, w);
+      }
       st.qop[ks] = qv;
     }
   }
@@ -667,18 +707,25 @@ paged_decode_kernel(const KParams p) {
           (L > 0.f) ? M + __log2f(L) : -INFINITY;
     }
   } else {
-    _Float16 *dst = reinterpret_cast<_Float16 *>(p.out) + (int64_t)b * p.sob + (int64_t)h * p.soh + d0;
-    if constexpr (kRegs >= 8) {
+    uint8_t *dst = p.out + ((int64_t)b * p.sob + (int64_t)h * p.soh + d0) * 2;
+    if (p.io_bf16) {
+      uint32_t w[kRegs / 2];
+#pragma unroll
+      for (int e = 0; e < kRegs / 2; ++e)
+        w[e] = f32_to_bf16_bits(y[2 * e]) | (f32_to_bf16_bits(y[2 * e + 1]) << 16);
+#pragma unroll
+      for (int e = 0; e < kRegs / 2; e += 2)
+        *reinterpret_cast<u32x2 *>(dst + 4 * e) = u32x2{w[e], w[e + 1]};
+    } else if constexpr (kRegs >= 8) {
 #pragma unroll
       for (int v8 = 0; v8 < kRegs / 8; ++v8) {
         f16x8 t8;
 #pragma unroll
         for (int e = 0; e < 8; ++e) t8[e] = (_Float16)y[8 * v8 + e];
-        *reinterpret_cast<f16x8 *>(dst + 8 * v8) = t8;
+        *reinterpret_cast<f16x8 *>(dst + 16 * v8) = t8;
       }
     } else {
-#pragma unroll
-      for (int e = 0; e < kRegs; ++e) dst[e] = (_Float16)y[e];
+      store_row(dst, y, kRegs, false);
     }
   }
 }
@@ -751,9 +798,17 @@ __global__ void __launch_bounds__(64) split_reduce_kernel(const RParams p) {
   for (int o = 32; o >= 1; o >>= 1) wsum += __shfl_xor(wsum, o);
   const float inv = (wsum > 0.f) ? 1.0f / wsum : 0.f;
   if (active) {
-    _Float16 *dst = reinterpret_cast<_Float16 *>(p.out) + (int64_t)b * p.sob + (int64_t)h * p.soh + lane * kPer;
+    uint8_t *dst = p.out + ((int64_t)b * p.sob + (int64_t)h * p.soh + lane * kPer) * 2;
+    float y[kPer];
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) dst[i] = (_Float16)(acc[i] * inv);
+    for (int i = 0; i < kPer; ++i) y[i] = acc[i] * inv;
+    if constexpr (kPer >= 2) {
+      store_row(dst, y, kPer, p.io_bf16 != 0);
+    } else {
+      const uint16_t bits = p.io_bf16 ? (uint16_t)f32_to_bf16_bits(y[0])
+                                      : __builtin_bit_cast(uint16_t, (_Float16)y[0]);
+      *reinterpret_cast<uint16_t *>(dst) = bits;
+    }
   }
 }
 
@@ -810,8 +865,10 @@ int build_params(const pa_decode_args *a, bool need_partials, KParams *kp) {
   if (a->max_seq_len < 0) return fail(PA_ERR_INVALID, "max_seq_len %d < 0", a->max_seq_len);
   if ((int64_t)a->max_blocks * a->block_size > 0x7fffffff)
     return fail(PA_ERR_UNSUPPORTED, "max_blocks * block_size exceeds 2^31 tokens");
-  if (a->io_dtype != PA_IO_FP16) return fail(PA_ERR_UNSUPPORTED, "io_dtype %d unsupported", a->io_dtype);
-  if (a->kv_dtype != PA_KV_FP16 && a->kv_dtype != PA_KV_FP8_E5M2 && a->kv_dtype != PA_KV_INT8)
+  if (a->io_dtype != PA_IO_FP16 && a->io_dtype != PA_IO_BF16)
+    return fail(PA_ERR_UNSUPPORTED, "io_dtype %d unsupported", a->io_dtype);
+  if (a->kv_dtype != PA_KV_FP16 && a->kv_dtype != PA_KV_FP8_E5M2 && a->kv_dtype != PA_KV_INT8 &&
+      a->kv_dtype != PA_KV_BF16)
     return fail(PA_ERR_INVALID, "kv_dtype %d unknown", a->kv_dtype);
   if (a->kv_dtype == PA_KV_INT8) {
     if (a->scale_dtype != PA_SCALE_FP16 && a->scale_dtype != PA_SCALE_FP32)
@@ -828,7 +885,7 @@ int build_params(const pa_decode_args *a, bool need_partials, KParams *kp) {
   if (need_partials && (!a->part_out || !a->part_lse))
     return fail(PA_ERR_INVALID, "num_splits > 1 needs part_out and part_lse");
 
-  const int elem = (a->kv_dtype == PA_KV_FP16) ? 2 : 1;
+  const int elem = (a->kv_dtype == PA_KV_FP16 || a->kv_dtype == PA_KV_BF16) ? 2 : 1;
   const int64_t strides[] = {a->stride_qb, a->stride_qh, a->stride_kn, a->stride_kt, a->stride_kh,
                              a->stride_ob, a->stride_oh, a->stride_btb};
   for (int64_t s : strides)
@@ -893,6 +950,7 @@ int build_params(const pa_decode_args *a, bool need_partials, KParams *kp) {
   k.slh = a->stride_lh;
   k.sbtb = a->stride_btb;
   k.qk_scale = a->sm_scale * kLog2e;
+  k.io_bf16 = a->io_dtype == PA_IO_BF16;
   return PA_OK;
 }
 
@@ -923,6 +981,7 @@ hipError_t launch_decode(const KParams &k, const pa_decode_args *a, int mode, hi
   const int grid = a->batch * a->num_kv_heads * k.head_tiles * a->num_splits;
   const int d = a->head_dim;
   if (a->kv_dtype == PA_KV_FP16) return launch_decode_d<PA_KV_FP16, PA_SCALE_NONE>(k, d, grid, mode, st);
+  if (a->kv_dtype == PA_KV_BF16) return launch_decode_d<PA_KV_BF16, PA_SCALE_NONE>(k, d, grid, mode, st);
   if (a->kv_dtype == PA_KV_FP8_E5M2)
     return launch_decode_d<PA_KV_FP8_E5M2, PA_SCALE_NONE>(k, d, grid, mode, st);
   if (a->scale_dtype == PA_SCALE_FP32) return launch_decode_d<PA_KV_INT8, PA_SCALE_FP32>(k, d, grid, mode, st);
@@ -938,7 +997,8 @@ int check_reduce(const pa_reduce_args *r, RParams *rp) {
                 r->num_heads, r->num_splits);
   if (r->head_dim != 32 && r->head_dim != 64 && r->head_dim != 128 && r->head_dim != 256)
     return fail(PA_ERR_UNSUPPORTED, "head_dim %d not in (32, 64, 128, 256)", r->head_dim);
-  if (r->io_dtype != PA_IO_FP16) return fail(PA_ERR_UNSUPPORTED, "io_dtype %d unsupported", r->io_dtype);
+  if (r->io_dtype != PA_IO_FP16 && r->io_dtype != PA_IO_BF16)
+    return fail(PA_ERR_UNSUPPORTED, "io_dtype %d unsupported", r->io_dtype);
   if (r->stride_pb < 0 || r->stride_ph < 0 || r->stride_ps < 0 || r->stride_lb < 0 ||
       r->stride_lh < 0 || r->stride_ob < 0 || r->stride_oh < 0)
     return fail(PA_ERR_INVALID, "strides must be non-negative");
@@ -947,6 +1007,7 @@ int check_reduce(const pa_reduce_args *r, RParams *rp) {
   rp->part_out = r->part_out;
   rp->part_lse = r->part_lse;
   rp->out = static_cast<uint8_t *>(r->out);
+  rp->io_bf16 = r->io_dtype == PA_IO_BF16;
   rp->seq_lens = nullptr;
   rp->max_tokens = 0;
   rp->max_seq_len = 0;

@@ -15,8 +15,8 @@ metadata (slot mapping, block tables, seq_lens) and the
 gives the NHD views the kernel reads in place.
 
 Differences from the reference:
-  * bf16 layers are delegated: the HIP kernel computes in fp16 and does not
-    silently down-cast bf16 (the reference feeds bf16 to an fp16 path).
+  * bf16 caches are served as the reference serves them (vllm_backend.py:132):
+    rows converted to fp16 in registers (round to nearest even), q/out bf16.
   * The classes are built by `build_backend_classes(base_backend, base_impl)`,
     so the routing is testable with stand-in base classes where vLLM is not
     installed; `install(platform_cls=...)` likewise accepts a stand-in platform.
@@ -64,7 +64,7 @@ def _reason_to_delegate(impl, attn_metadata, kv_cache, output, output_scale) -> 
     """Why a forward call must go to vLLM's own attention ("" = ours).
 
     The reference's list (vllm_backend.py:67-90), in its order, plus one rule
-    of this build: only fp16 caches are served here.
+    of this build: only fp16 and bf16 caches are served here.
     """
     checks = (
         (attn_metadata is None, "profiling run (no metadata)"),
@@ -78,7 +78,8 @@ def _reason_to_delegate(impl, attn_metadata, kv_cache, output, output_scale) -> 
         (getattr(attn_metadata, "local_attn_metadata", None) is not None, "local (iRoPE) attention"),
         (bool(getattr(attn_metadata, "use_cascade", False)), "cascade attention"),
         (getattr(attn_metadata, "max_query_len", 2) != 1, "not a pure-decode batch"),
-        (kv_cache is not None and kv_cache.dtype != torch.float16, "cache dtype is not fp16"),
+        (kv_cache is not None and kv_cache.dtype not in (torch.float16, torch.bfloat16),
+         "cache dtype is not fp16 or bf16"),
     )
     for hit, why in checks:
         if hit:
@@ -98,8 +99,8 @@ def _write_kv(layer, impl, key, value, key_cache, value_cache, slot_mapping) -> 
     """This step's K/V into the paged cache (vllm_backend.py:117-122).
 
     vLLM's own op when it is loaded; otherwise this library's HIP writer,
-    which stores the same bytes for the fp16 caches this backend serves
-    (`_reason_to_delegate` sends every other cache dtype to vLLM).
+    which stores the same bytes for the fp16 / bf16 caches this backend
+    serves (`_reason_to_delegate` sends every other cache dtype to vLLM).
     """
     op = _vllm_cache_op()
     if op is not None:
@@ -111,9 +112,15 @@ def _write_kv(layer, impl, key, value, key_cache, value_cache, slot_mapping) -> 
     n = int(slot_mapping.shape[0])
     view = PagedKVCache(
         shape=ModelShape(impl.num_heads, impl.num_kv_heads, impl.head_size, name="vllm"),
-        block_size=int(key_cache.shape[1]), kv_dtype="fp16", k_cache=key_cache,
+        block_size=int(key_cache.shape[1]), kv_dtype=_kv_dtype_of(key_cache), k_cache=key_cache,
         v_cache=value_cache, k_scale=None, v_scale=None, block_table=None, seq_lens=None)
     reshape_and_cache(key[:n], value[:n], view, slot_mapping.to(torch.int64))
+
+
+def _kv_dtype_of(cache: torch.Tensor) -> str:
+    """The reference's mapping (vllm_backend.py:132): bf16 caches are served
+    through the fp16 arithmetic, fp16 as is."""
+    return "bf16" if cache.dtype == torch.bfloat16 else "fp16"
 
 
 _CU_COUNT: dict[int, int] = {}
@@ -137,7 +144,7 @@ def decode_forward(impl, layer, query, key, value, kv_cache, attn_metadata, outp
     cache = PagedKVCache(
         shape=ModelShape(impl.num_heads, impl.num_kv_heads, impl.head_size, name="vllm"),
         block_size=int(key_cache.shape[1]),
-        kv_dtype="fp16",
+        kv_dtype=_kv_dtype_of(key_cache),
         k_cache=key_cache,
         v_cache=value_cache,
         k_scale=None,

@@ -22,12 +22,14 @@ PA_ERR_HIP = -3
 PA_KV_FP16 = 0
 PA_KV_FP8_E5M2 = 1
 PA_KV_INT8 = 2
+PA_KV_BF16 = 3
 
 PA_SCALE_NONE = 0
 PA_SCALE_FP16 = 1
 PA_SCALE_FP32 = 2
 
 PA_IO_FP16 = 0
+PA_IO_BF16 = 1
 
 PA_MAX_SPLITS = 4096
 PA_MAX_GROUP = 16

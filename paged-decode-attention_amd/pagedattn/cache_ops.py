@@ -19,8 +19,10 @@ import torch
 from . import _abi
 from .cache import PagedKVCache
 
-_KV_CODE = {"fp16": _abi.PA_KV_FP16, "fp8_e5m2": _abi.PA_KV_FP8_E5M2, "int8": _abi.PA_KV_INT8}
-_STORE_DTYPE = {"fp16": torch.float16, "fp8_e5m2": torch.float8_e5m2, "int8": torch.int8}
+_KV_CODE = {"fp16": _abi.PA_KV_FP16, "fp8_e5m2": _abi.PA_KV_FP8_E5M2, "int8": _abi.PA_KV_INT8,
+            "bf16": _abi.PA_KV_BF16}
+_STORE_DTYPE = {"fp16": torch.float16, "fp8_e5m2": torch.float8_e5m2, "int8": torch.int8,
+                "bf16": torch.bfloat16}
 _SCALE_CODE = {torch.float16: _abi.PA_SCALE_FP16, torch.float32: _abi.PA_SCALE_FP32}
 
 
@@ -40,8 +42,10 @@ def reshape_and_cache(
     n, h, d = key.shape
     if key.device.type != "cuda":
         raise ValueError(f"key is on {key.device}: the HIP cache writer needs GPU tensors")
-    if key.dtype != torch.float16 or value.dtype != torch.float16:
-        raise NotImplementedError(f"key/value dtype {key.dtype}/{value.dtype}: only float16 is supported")
+    row_dtype = torch.bfloat16 if cache.kv_dtype == "bf16" else torch.float16
+    if key.dtype != row_dtype or value.dtype != row_dtype:
+        raise NotImplementedError(f"key/value dtype {key.dtype}/{value.dtype}: a {cache.kv_dtype} cache "
+                                  f"takes {row_dtype} rows")
     if tuple(value.shape) != (n, h, d) or h != cache.shape.num_kv_heads or d != cache.shape.head_dim:
         raise ValueError(f"key {tuple(key.shape)} / value {tuple(value.shape)} do not match the cache's "
                          f"[{cache.shape.num_kv_heads}, {cache.shape.head_dim}] rows")

@@ -34,8 +34,11 @@ RESIDENT_WORKGROUPS_PER_CU = 2
 # Smallest split chunk worth a workgroup (16 tiles, 4 per wave).
 MIN_SPLIT_TOKENS = 512
 
-_KV_CODE = {"fp16": _abi.PA_KV_FP16, "fp8_e5m2": _abi.PA_KV_FP8_E5M2, "int8": _abi.PA_KV_INT8}
-_STORE_DTYPE = {"fp16": torch.float16, "fp8_e5m2": torch.float8_e5m2, "int8": torch.int8}
+_KV_CODE = {"fp16": _abi.PA_KV_FP16, "fp8_e5m2": _abi.PA_KV_FP8_E5M2, "int8": _abi.PA_KV_INT8,
+            "bf16": _abi.PA_KV_BF16}
+_STORE_DTYPE = {"fp16": torch.float16, "fp8_e5m2": torch.float8_e5m2, "int8": torch.int8,
+                "bf16": torch.bfloat16}
+_IO_CODE = {torch.float16: _abi.PA_IO_FP16, torch.bfloat16: _abi.PA_IO_BF16}
 _SCALE_CODE = {torch.float16: _abi.PA_SCALE_FP16, torch.float32: _abi.PA_SCALE_FP32}
 
 
@@ -121,8 +124,8 @@ def _fill_args(
     shape = cache.shape
     if cache.kv_dtype not in _KV_CODE:
         raise NotImplementedError(f"kv_dtype {cache.kv_dtype!r} is not supported by the HIP kernel")
-    if q.dtype != torch.float16 or out.dtype != torch.float16:
-        raise NotImplementedError(f"q/out dtype {q.dtype}/{out.dtype}: only float16 is supported")
+    if q.dtype not in _IO_CODE or out.dtype != q.dtype:
+        raise NotImplementedError(f"q/out dtype {q.dtype}/{out.dtype}: float16 or bfloat16, the same for both")
     if q.device.type != "cuda":
         raise ValueError(f"q is on {q.device}: the HIP decode kernel needs GPU tensors")
     k, v = cache.k_cache, cache.v_cache
@@ -170,7 +173,7 @@ def _fill_args(
     a.stride_ob, a.stride_oh = out.stride(0), out.stride(1)
     a.stride_btb = bt.stride(0)
     a.kv_dtype = _KV_CODE[cache.kv_dtype]
-    a.io_dtype = _abi.PA_IO_FP16
+    a.io_dtype = _IO_CODE[q.dtype]
     a.sm_scale = sm_scale
     if cache.kv_dtype == "int8":
         ks, vs = cache.k_scale, cache.v_scale
@@ -213,7 +216,7 @@ def paged_decode_hip(
     sm_scale: float | None = None,
     max_seq_len: int | None = None,
 ) -> torch.Tensor:
-    """Paged GQA decode attention. q: [B, Hq, D] fp16 -> [B, Hq, D] fp16.
+    """Paged GQA decode attention. q: [B, Hq, D] fp16|bf16 -> [B, Hq, D] in q's dtype.
 
     Reference: pagedattn/triton_decode.py:285-377. `sm_scale` overrides the
     default 1/sqrt(head_dim) (a serving runtime may fold other factors in).
@@ -301,7 +304,7 @@ def decode_partials(
 def split_reduce(
     part_out: torch.Tensor, part_lse: torch.Tensor, out: torch.Tensor | None = None
 ) -> torch.Tensor:
-    """Merge split partials into [B, H, D] fp16 (triton_decode.py:198-240)."""
+    """Merge split partials into [B, H, D] fp16 or bf16 (triton_decode.py:198-240)."""
     b, h, s, d = part_out.shape
     if part_out.dtype != torch.float32 or part_lse.dtype != torch.float32:
         raise ValueError("partials must be float32")
@@ -309,8 +312,8 @@ def split_reduce(
         raise ValueError("part_out must have a contiguous head dim and part_lse shape [B, H, S]")
     if out is None:
         out = torch.empty((b, h, d), dtype=torch.float16, device=part_out.device)
-    if out.dtype != torch.float16 or out.stride(2) != 1:
-        raise ValueError("out must be float16 with a contiguous head dim")
+    if out.dtype not in _IO_CODE or out.stride(2) != 1:
+        raise ValueError("out must be float16 or bfloat16 with a contiguous head dim")
     r = _abi.PaReduceArgs()
     r.part_out = part_out.data_ptr()
     r.part_lse = part_lse.data_ptr()
@@ -319,7 +322,7 @@ def split_reduce(
     r.stride_pb, r.stride_ph, r.stride_ps = part_out.stride(0), part_out.stride(1), part_out.stride(2)
     r.stride_lb, r.stride_lh = part_lse.stride(0), part_lse.stride(1)
     r.stride_ob, r.stride_oh = out.stride(0), out.stride(1)
-    r.io_dtype = _abi.PA_IO_FP16
+    r.io_dtype = _IO_CODE[out.dtype]
     lib = _abi.load()
     with torch.cuda.device(part_out.device):
         rc = lib.pa_split_reduce(ctypes.byref(r), _stream(part_out.device))

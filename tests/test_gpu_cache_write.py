@@ -111,3 +111,16 @@ def test_write_then_decode(kv_dtype):
     torch.cuda.synchronize()
     want = oracle.reference_decode(q, ref, out_dtype=torch.float32)
     assert max_abs(got, want) < 2e-3
+
+
+def test_bf16_rows_into_bf16_cache():
+    c = allocate(LLAMA3_8B, 1, [64], kv_dtype="bf16", seed=46, device="cuda", slack_blocks=2)
+    ref = _cpu_copy(c)
+    g = torch.Generator().manual_seed(47)
+    key = torch.randn((5, 8, 128), generator=g).to(torch.bfloat16)
+    value = torch.randn((5, 8, 128), generator=g).to(torch.bfloat16)
+    slots = torch.tensor([0, 17, -1, 40, 95], dtype=torch.int64)
+    reshape_and_cache(key.cuda(), value.cuda(), c, slots.cuda())
+    oracle.write_kv(key, value, ref, slots)
+    torch.cuda.synchronize()
+    assert torch.equal(c.k_cache.cpu(), ref.k_cache) and torch.equal(c.v_cache.cpu(), ref.v_cache)

@@ -269,3 +269,45 @@ def test_auto_split_count():
     q, c = _qkv(1, 5000, seed=16)
     ref = oracle.reference_decode(q, c, out_dtype=torch.float32)
     _check(paged_decode_hip(q, c), ref)
+
+
+# bf16 output is rounded to bf16 (8-bit significand): half an ulp of |ref| on
+# top of the kernel's own 2e-3 bar
+def _check_bf16(got, ref):
+    torch.cuda.synchronize()
+    assert got.dtype == torch.bfloat16
+    err = (got.float().cpu() - ref.float().cpu()).abs()
+    bound = ABS_TOL + 2.0 ** -8 * ref.float().cpu().abs()
+    print(f"bf16 max_abs={err.max().item():.2e} worst margin={(err - bound).max().item():.2e}")
+    assert bool((err <= bound).all()), f"bf16 error above bound by {(err - bound).max().item():.3e}"
+
+
+@pytest.mark.parametrize("kv_dtype", ["bf16", "fp16", "fp8_e5m2", "int8"])
+@pytest.mark.parametrize("num_splits", [1, 5])
+def test_bf16_q_and_out(kv_dtype, num_splits):
+    """bf16 q/out (converted in registers; the reference maps bf16 onto its
+    fp16 path, triton_decode.py:30,151-153) with every KV dtype."""
+    lens = [1, 300, 2049]
+    c = allocate(LLAMA3_8B, 3, lens, kv_dtype=kv_dtype, seed=19, device="cuda")
+    q = seeded_q(3, 32, 128, 19, device="cuda").to(torch.bfloat16)
+    ref = oracle.reference_decode(q, c, out_dtype=torch.float32)
+    got = paged_decode_hip(q, c, num_splits=num_splits)
+    _check_bf16(got, ref)
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(14, 2, 64), (8, 2, 32), (16, 4, 256)])
+def test_bf16_cache_fp16_q(hq, hkv, d):
+    shape = ModelShape(hq, hkv, d, name=f"{hq}x{hkv}x{d}")
+    q, c = _qkv(2, 333, shape=shape, seed=20, kv_dtype="bf16")
+    ref = oracle.reference_decode(q, c, out_dtype=torch.float32)
+    for ns in (1, 3):
+        _check(paged_decode_hip(q, c, num_splits=ns), ref)
+
+
+def test_bf16_split_reduce_output():
+    lens = [700, 40]
+    c = allocate(LLAMA3_8B, 2, lens, kv_dtype="bf16", seed=21, device="cuda")
+    q = seeded_q(2, 32, 128, 21, device="cuda").to(torch.bfloat16)
+    po, pl = decode_partials(q, c, 4)
+    out = split_reduce(po, pl, torch.empty((2, 32, 128), dtype=torch.bfloat16, device="cuda"))
+    _check_bf16(out, oracle.reference_decode(q, c, out_dtype=torch.float32))

@@ -100,3 +100,22 @@ def test_impl_forward_matches_oracle(shape, lens):
     assert err < 2e-3
     assert torch.equal(output[n:], torch.full_like(output[n:], 7.0))
     assert vb.STATS["decode_calls"] >= 1
+
+
+def test_impl_forward_bf16_cache():
+    """bf16 models: the reference serves bf16 caches through its fp16 path
+    (vllm_backend.py:132); so does this backend, with bf16 q/out."""
+    _, Impl = vb.build_backend_classes(object, _BaseImpl)
+    lens = [70, 5]
+    c = allocate(LLAMA3_8B, 2, lens, kv_dtype="bf16", seed=34, device="cuda")
+    kv_cache = torch.stack([c.k_cache, c.v_cache])
+    meta = types.SimpleNamespace(max_query_len=1, num_actual_tokens=2, use_cascade=False,
+                                 local_attn_metadata=None, max_seq_len=70, block_table=c.block_table,
+                                 seq_lens=c.seq_lens, slot_mapping=None)
+    query = seeded_q(2, 32, 128, 34, device="cuda").to(torch.bfloat16)
+    output = torch.zeros_like(query)
+    Impl(LLAMA3_8B).forward(None, query, None, None, kv_cache, meta, output)
+    torch.cuda.synchronize()
+    want = oracle.reference_decode(query, c, out_dtype=torch.float32)
+    err = (output.float().cpu() - want).abs()
+    assert bool((err <= 2e-3 + 2.0 ** -8 * want.abs()).all())

@@ -82,7 +82,8 @@ def test_constants_match_header():
     text = HEADER.read_text()
     for name in ("PA_ABI_VERSION", "PA_OK", "PA_ERR_INVALID", "PA_ERR_UNSUPPORTED", "PA_ERR_HIP",
                  "PA_KV_FP16", "PA_KV_FP8_E5M2", "PA_KV_INT8", "PA_SCALE_NONE", "PA_SCALE_FP16",
-                 "PA_SCALE_FP32", "PA_IO_FP16", "PA_MAX_SPLITS", "PA_MAX_GROUP"):
+                 "PA_SCALE_FP32", "PA_IO_FP16", "PA_MAX_SPLITS", "PA_MAX_GROUP", "PA_KV_BF16",
+                 "PA_IO_BF16"):
         m = re.search(rf"#define {name} \(?(-?\d+)\)?", text)
         assert m, name
         assert int(m.group(1)) == getattr(_abi, name), name
@@ -128,6 +129,7 @@ INVALID = [
     ("no_workspace", dict(num_splits=4), _abi.PA_ERR_INVALID),
     ("kv_dtype", dict(kv_dtype=7), _abi.PA_ERR_INVALID),
     ("io_dtype", dict(io_dtype=3), _abi.PA_ERR_UNSUPPORTED),
+    ("bf16_scale", dict(kv_dtype=_abi.PA_KV_BF16, scale_dtype=_abi.PA_SCALE_FP16), _abi.PA_ERR_INVALID),
     ("int8_no_scale", dict(kv_dtype=_abi.PA_KV_INT8, scale_dtype=_abi.PA_SCALE_FP16), _abi.PA_ERR_INVALID),
     ("int8_scale_type", dict(kv_dtype=_abi.PA_KV_INT8, k_scale=FAKE, v_scale=FAKE), _abi.PA_ERR_INVALID),
     ("scale_on_fp16", dict(scale_dtype=_abi.PA_SCALE_FP32), _abi.PA_ERR_INVALID),

@@ -115,6 +115,8 @@ CASES = [
     (ModelShape(16, 2, 64, "g8"), [129, 3], "int8", 16, torch.float16),
     (ModelShape(64, 8, 128, "70b"), [70], "int8", 16, torch.float32),
     (ModelShape(24, 1, 256, "d256"), [50, 1], "int8", 32, torch.float32),
+    (LLAMA3_8B, [90, 7], "bf16", 16, torch.float16),
+    (ModelShape(14, 2, 64, "qwen"), [33], "bf16", 32, torch.float16),
 ]
 
 
@@ -503,3 +505,20 @@ def test_write_then_decode_reads_the_new_token():
     out = oracle.reference_decode(q, c, out_dtype=torch.float32)
     for h in range(8):
         assert (out[0, h] - value[0, h // 4].float()).abs().max().item() < 1e-3
+
+
+def test_bf16_rows_are_read_as_fp16():
+    """A bf16 cache is attended through fp16 (the reference's bf16 path,
+    triton_decode.py:30,151 and cache.py:55-56): values that bf16 holds but
+    fp16 rounds come out rounded, and the C oracle agrees."""
+    c = _cache(LLAMA3_8B, [1], "bf16", seed=25)
+    vals = torch.tensor([1 + 2 ** -7, 1e-8, 70000.0, 1.0 + 2 ** -8 + 2 ** -9], dtype=torch.bfloat16)
+    c.v_cache[int(c.block_table[0, 0]), 0, 0, :4] = vals
+    q = _q(1, 32, 128, 25)
+    out = oracle.reference_decode(q, c, out_dtype=torch.float32)
+    # bf16 -> fp16 with torch's cast: exact, underflow to 0, overflow to inf, exact
+    want = vals.to(torch.float16).float()
+    assert want[1] == 0 and torch.isinf(want[2]) and want[0] == 1 + 2 ** -7
+    assert torch.equal(out[0, 0, :4], want)
+    got_c = c_oracle.decode(q, c).float()
+    assert torch.equal(got_c[0, 0, :4], want)

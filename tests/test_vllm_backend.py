@@ -79,13 +79,13 @@ def test_supports_shape():
     ({}, {"local_attn_metadata": object()}, "kv", "out", None, "local (iRoPE) attention"),
     ({}, {"use_cascade": True}, "kv", "out", None, "cascade attention"),
     ({}, {"max_query_len": 7}, "kv", "out", None, "not a pure-decode batch"),
-    ({}, {}, "bf16", "out", None, "cache dtype is not fp16"),
+    ({}, {}, "f32", "out", None, "cache dtype is not fp16 or bf16"),
     ({}, {}, "kv", "out", None, ""),
 ])
 def test_reason_to_delegate(impl_over, meta_over, kv, out, scale, expect):
     impl = FakeBaseImpl(**impl_over)
     meta = None if meta_over is None else _meta(**meta_over)
-    kv_cache = {"kv": _kv(), "empty": torch.zeros(0), "bf16": _kv(torch.bfloat16)}[kv]
+    kv_cache = {"kv": _kv(), "empty": torch.zeros(0), "f32": _kv(torch.float32)}[kv]
     output = torch.zeros(2, 32, 128, dtype=torch.float16) if out else None
     assert vb._reason_to_delegate(impl, meta, kv_cache, output, scale) == expect
 
