@@ -252,7 +252,7 @@ def main() -> int:
 
     import torch
 
-    from pagedattn import allocate, pick_num_splits
+    from pagedattn import allocate, plan_num_splits
     from pagedattn.hip_decode import _WS, _cu_count, decode_partials, paged_decode_hip
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
@@ -285,7 +285,8 @@ def main() -> int:
         return bench_write(args, wl, shape, cache, dev)
 
     cus = _cu_count(dev)
-    splits = args.splits or pick_num_splits(wl.batch, shape.num_kv_heads, max(wl.lens), cus)
+    # the workload's lengths are known here, so the exact planner decides
+    splits = args.splits or plan_num_splits(wl.lens, shape.num_kv_heads, shape.gqa_group, cus)[0]
     out = torch.empty_like(q)
     algo = _algorithmic_bytes(cache)
     kv_only = cache.bytes_read_per_decode_step()

@@ -263,9 +263,11 @@ struct Geo {
   static constexpr int kKSlotStride = kRowBytes + 16;       // padded LDS row
   static constexpr int kKSlotBytes = kTT * kKSlotStride;    // per wave
   static constexpr int kScales = 2 * kTT;                   // int8: K and V scales per tile
-  // double-buffer the tile registers unless they would crowd out the rest
+  // double-buffer the tile registers unless, with the accumulators and the Q
+  // operands, they would crowd out the rest (the budget is set by the
+  // largest instance that measured best double-buffered: fp16 at D = 128)
   static constexpr int kTileWords = 4 * kKLoads + kVRows * kVWords;
-  static constexpr bool kPrefetch = kTileWords <= 64;
+  static constexpr bool kPrefetch = 2 * kTileWords + 4 * kE + 4 * kKSteps <= 176;
 };
 
 // Registers of one tile of one wave.
@@ -382,8 +384,10 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  // ---- int8 scales of this lane's tokens {16u + 4c + i} via LDS ----
-  float ksc[NV], vsc[NV];
+  // ---- int8 scales of this lane's tokens {16u + 4c + i} via LDS (the V
+  // scales are read back only for the P operand, to keep them out of the
+  // registers live across the QK products) ----
+  float ksc[NV];
   if constexpr (KV == PA_KV_INT8) {
 #pragma unroll
     for (int j = 0; j < G::kScales / 64; ++j) sc_lds[j * 64 + lane] = r.sc[j];
@@ -393,16 +397,9 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
 #pragma unroll
     for (int u = 0; u < NS; ++u) {
       const f32x4 kq = *reinterpret_cast<const f32x4 *>(sc_lds + 16 * u + 4 * c);
-      const f32x4 vq = *reinterpret_cast<const f32x4 *>(sc_lds + 16 * (NS + u) + 4 * c);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        ksc[4 * u + i] = kq[i];
-        vsc[4 * u + i] = vq[i];
-      }
+      for (int i = 0; i < 4; ++i) ksc[4 * u + i] = kq[i];
     }
-    // the next tile's scales overwrite the slot only after these reads
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
   }
 
   // ---- S^T = K Q^T, one 16-token sub-tile at a time ----
@@ -477,11 +474,17 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
 #pragma unroll
   for (int pp = 0; pp < NS / 2; ++pp) {
     f16x8 pop;
+    if constexpr (KV == PA_KV_INT8) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float x = pr[8 * pp + e];
-      if constexpr (KV == PA_KV_INT8) x *= vsc[8 * pp + e];
-      pop[e] = (_Float16)x;
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const int u = 2 * pp + h2;
+        const f32x4 vq = *reinterpret_cast<const f32x4 *>(sc_lds + 16 * (NS + u) + 4 * c);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pop[4 * h2 + i] = (_Float16)(pr[4 * u + i] * vq[i]);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pop[e] = (_Float16)pr[8 * pp + e];
     }
 #pragma unroll
     for (int sl = 0; sl < G::kE; ++sl) {
@@ -504,6 +507,11 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
       const f16x8 vop = finish<KV>(as_f16x8(h[0], h[1], h[2], h[3]));
       st.acc[sl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop, st.acc[sl], 0, 0, 0);
     }
+  }
+  if constexpr (KV == PA_KV_INT8) {
+    // the next tile's scales overwrite the slot only after these reads
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
@@ -567,8 +575,18 @@ paged_decode_kernel(const KParams p) {
   const int r16 = lane & 15;
   const int c = lane >> 4;
 
-  // blockIdx.x = ((b * hkv + kvh) * head_tiles + ht) * num_splits + split
-  int x = blockIdx.x;
+  // With splits, XCD x (the hardware deals workgroups round-robin to the 8
+  // XCDs) takes the contiguous logical range [x * n / 8, (x + 1) * n / 8) of
+  // (b, kv_head, head_tile, split) = all splits of a few sequences: measured
+  // 3-33% faster on split workloads (ragged most), 2% slower unsplit, so only
+  // split launches remap. The tail past a multiple of 8 keeps its index.
+  int wg = blockIdx.x;
+  if (MODE != kUnsplit) {
+    const int n = gridDim.x, full = n - n % 8;
+    if (wg < full) wg = (wg % 8) * (full / 8) + wg / 8;
+  }
+  // wg = ((b * hkv + kvh) * head_tiles + ht) * num_splits + split
+  int x = wg;
   const int split = x % p.num_splits;
   x /= p.num_splits;
   const int ht = x % p.head_tiles;

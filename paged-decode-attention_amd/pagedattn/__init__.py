@@ -15,6 +15,7 @@ from .hip_decode import (
     paged_decode_hip,
     paged_decode_triton,
     pick_num_splits,
+    plan_num_splits,
     split_reduce,
 )
 
@@ -22,6 +23,6 @@ __all__ = [
     "LLAMA3_8B", "LLAMA3_70B", "MHA_DEBUG", "QWEN25_05B", "KVDType", "ModelShape",
     "kv_bytes_per_token",
     "PagedKVCache", "allocate", "quantize_kv", "reshape_and_cache",
-    "paged_decode_hip", "paged_decode_triton", "pick_num_splits",
+    "paged_decode_hip", "paged_decode_triton", "pick_num_splits", "plan_num_splits",
     "decode_partials", "split_reduce",
 ]

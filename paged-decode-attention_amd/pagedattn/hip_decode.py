@@ -33,6 +33,9 @@ TILE_TOKENS = 32
 RESIDENT_WORKGROUPS_PER_CU = 2
 # Smallest split chunk worth a workgroup (16 tiles, 4 per wave).
 MIN_SPLIT_TOKENS = 512
+# Rounds of resident workgroups a split launch is planned for (measured on
+# the BASELINE ragged / long-context shapes: 2 beats 1 and 3).
+SPLIT_ROUNDS = 2
 
 _KV_CODE = {"fp16": _abi.PA_KV_FP16, "fp8_e5m2": _abi.PA_KV_FP8_E5M2, "int8": _abi.PA_KV_INT8,
             "bf16": _abi.PA_KV_BF16}
@@ -66,6 +69,34 @@ def pick_num_splits(
     want = -(-2 * slots // base)
     max_useful = max(1, max_seq_len // MIN_SPLIT_TOKENS)
     return int(max(1, min(want, max_useful, _abi.PA_MAX_SPLITS)))
+
+
+def plan_num_splits(seq_lens, num_kv_heads: int, group: int, sm_count: int) -> tuple[int, int]:
+    """(num_splits, max_seq_len) for a batch whose lengths the host knows.
+
+    `pick_num_splits` sees only the longest length, so it cannot tell a
+    uniform batch (best unsplit when it already fills the CUs) from a ragged
+    one (whose long sequences then run alone at the end). With the lengths:
+      * nearly uniform (longest <= 1.25 x mean) and every CU holds its
+        resident workgroups: no split;
+      * otherwise the balanced chunking (every sequence cut with the longest
+        one's chunk) with about SPLIT_ROUNDS rounds of resident workgroups of
+        work: chunk ~ sum(T) * heads / (SPLIT_ROUNDS * slots), at least
+        MIN_SPLIT_TOKENS.
+    """
+    lens = [max(0, int(t)) for t in seq_lens]
+    if not lens or max(lens) == 0:
+        return 1, 0
+    tmax = max(lens)
+    head_tiles = -(-group // _abi.PA_MAX_GROUP)
+    units = num_kv_heads * head_tiles
+    slots = RESIDENT_WORKGROUPS_PER_CU * max(1, sm_count)
+    mean = sum(lens) / len(lens)
+    if len(lens) * units >= slots and tmax <= 1.25 * mean:
+        return 1, tmax
+    chunk = max(MIN_SPLIT_TOKENS, sum(lens) * units // (SPLIT_ROUNDS * slots))
+    splits = max(1, min(-(-tmax // chunk), _abi.PA_MAX_SPLITS))
+    return int(splits), tmax
 
 
 class _Workspace:
@@ -220,10 +251,10 @@ def paged_decode_hip(
 
     Reference: pagedattn/triton_decode.py:285-377. `sm_scale` overrides the
     default 1/sqrt(head_dim) (a serving runtime may fold other factors in).
-    With `num_splits=None` the split count comes from `pick_num_splits`, which
-    needs `seq_lens.max()` on the host (a device sync, as in the reference);
-    serving callers pass `num_splits` to avoid it. A sequence with
-    seq_len == 0 produces zeros.
+    With `num_splits=None` the split count comes from `plan_num_splits` on the
+    lengths, read on the host in one device sync (the reference syncs there
+    too, for `seq_lens.max()`); serving callers pass `num_splits` to avoid
+    it. A sequence with seq_len == 0 produces zeros.
 
     `max_seq_len` (an addition; a host int such as vLLM's
     `attn_metadata.max_seq_len`) sizes every sequence's split chunk from the
@@ -248,10 +279,10 @@ def paged_decode_hip(
     if b == 0:
         return out
     if num_splits is None:
-        max_seq = int(cache.seq_lens.max().item())
-        num_splits = pick_num_splits(b, hkv, max_seq, _cu_count(q.device), block_n)
+        # the lengths come to the host in the one sync the reference also makes
+        num_splits, longest = plan_num_splits(cache.seq_lens.tolist(), hkv, group, _cu_count(q.device))
         if max_seq_len is None:
-            max_seq_len = max_seq
+            max_seq_len = longest
     num_splits = int(num_splits)
     scale = shape.softmax_scale if sm_scale is None else float(sm_scale)
 
@@ -332,8 +363,8 @@ def split_reduce(
 
 def split_count_for(cache: PagedKVCache, device: torch.device) -> int:
     """The split count `paged_decode_hip(num_splits=None)` would choose."""
-    max_seq = int(cache.seq_lens.max().item()) if cache.batch else 0
-    return pick_num_splits(cache.batch, cache.shape.num_kv_heads, max_seq, _cu_count(device))
+    return plan_num_splits(cache.seq_lens.tolist(), cache.shape.num_kv_heads, cache.shape.gqa_group,
+                           _cu_count(device))[0]
 
 
 __all__ = [
@@ -343,6 +374,7 @@ __all__ = [
     "decode_partials",
     "split_reduce",
     "split_count_for",
+    "plan_num_splits",
     "WAVES_PER_WORKGROUP",
     "TILE_TOKENS",
 ]

@@ -303,3 +303,25 @@ def test_algorithmic_bytes_of_baseline_configs():
     assert bench._algorithmic_bytes(fake(LLAMA3_8B, [4096] * 64, "fp16")) == 1_074_855_936
     assert bench._algorithmic_bytes(fake(LLAMA3_70B, [16384] * 32, "int8", torch.float32)) == 1_108_475_904
     assert bench._algorithmic_bytes(fake(LLAMA3_8B, [131072] * 4, "fp16")) == 2_147_680_256
+
+
+def test_plan_num_splits():
+    from pagedattn import plan_num_splits
+
+    # uniform batches that fill the CUs stay unsplit (the headline shape)
+    assert plan_num_splits([4096] * 64, 8, 4, 256) == (1, 4096)
+    # a ragged batch of the same size splits its long sequences
+    import math
+
+    g = torch.Generator().manual_seed(2)
+    u = torch.rand(64, generator=g, dtype=torch.float64)
+    ragged = torch.exp(math.log(128) + u * (math.log(8192) - math.log(128))).round().long().tolist()
+    s, m = plan_num_splits(ragged, 8, 4, 256)
+    assert s >= 4 and m == max(ragged)
+    # small batches of long sequences: many splits (BASELINE C5: >= 32)
+    assert plan_num_splits([131072] * 4, 8, 4, 256)[0] >= 32
+    assert plan_num_splits([16384] * 32, 8, 8, 256)[0] >= 4
+    # edge cases
+    assert plan_num_splits([], 8, 4, 256) == (1, 0)
+    assert plan_num_splits([0, 0], 8, 4, 256) == (1, 0)
+    assert plan_num_splits([1], 1, 1, 256)[0] == 1
