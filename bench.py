@@ -242,6 +242,8 @@ def main() -> int:
     ap.add_argument("--op", default="decode", choices=["decode", "write"],
                     help="decode (the headline) or write: the KV-cache write of --write-tokens rows")
     ap.add_argument("--write-tokens", type=int, default=65536)
+    ap.add_argument("--flat", type=int, default=None,
+                    help="flat (work-balanced) split with this many ranges per kv head; 0 = classic")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -252,7 +254,7 @@ def main() -> int:
 
     import torch
 
-    from pagedattn import allocate, plan_num_splits
+    from pagedattn import allocate, flat_workgroups_per_cu, plan_decode, plan_num_splits
     from pagedattn.hip_decode import _WS, _cu_count, decode_partials, paged_decode_hip
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
@@ -286,19 +288,26 @@ def main() -> int:
 
     cus = _cu_count(dev)
     # the workload's lengths are known here, so the exact planner decides
-    splits = args.splits or plan_num_splits(wl.lens, shape.num_kv_heads, shape.gqa_group, cus)[0]
+    # unless --splits / --flat force a launch shape
+    wgs = flat_workgroups_per_cu(wl.kv_dtype, shape.head_dim,
+                                 torch.float32 if wl.scale_fp32 else torch.float16)
+    splits, _, flat = plan_decode(wl.lens, shape.num_kv_heads, shape.gqa_group, cus, wgs)
+    if args.flat is not None or args.splits:
+        flat = int(args.flat or 0)
+        splits = 1 if flat else (args.splits or
+                                 plan_num_splits(wl.lens, shape.num_kv_heads, shape.gqa_group, cus)[0])
     out = torch.empty_like(q)
     algo = _algorithmic_bytes(cache)
     kv_only = cache.bytes_read_per_decode_step()
-    _log(f"{cus} CUs, num_splits={splits}, algorithmic bytes/call={algo}")
+    _log(f"{cus} CUs, num_splits={splits}, flat_splits={flat}, algorithmic bytes/call={algo}")
 
     # parity on a sample of sequences against the CPU oracle, and bit stability
     from oracle import reference as oracle
 
     msl = max(wl.lens)
-    paged_decode_hip(q, cache, out=out, num_splits=splits, max_seq_len=msl)
+    paged_decode_hip(q, cache, out=out, num_splits=splits, max_seq_len=msl, flat_splits=flat)
     first = out.clone()
-    paged_decode_hip(q, cache, out=out, num_splits=splits, max_seq_len=msl)
+    paged_decode_hip(q, cache, out=out, num_splits=splits, max_seq_len=msl, flat_splits=flat)
     torch.cuda.synchronize()
     bit_stable = bool(torch.equal(first, out))
     rows = sorted({0, wl.batch // 2, wl.batch - 1})
@@ -319,13 +328,15 @@ def main() -> int:
 
     # whole-call timing (decode + reduce when split), rotating pool copies
     for i in range(args.warmup):
-        paged_decode_hip(q, caches[i % copies], out=out, num_splits=splits, max_seq_len=msl)
+        paged_decode_hip(q, caches[i % copies], out=out, num_splits=splits, max_seq_len=msl,
+                         flat_splits=flat)
     torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     ev0.record()
     t_wall = time.perf_counter()
     for i in range(args.steps):
-        paged_decode_hip(q, caches[i % copies], out=out, num_splits=splits, max_seq_len=msl)
+        paged_decode_hip(q, caches[i % copies], out=out, num_splits=splits, max_seq_len=msl,
+                         flat_splits=flat)
     ev1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_wall
@@ -333,7 +344,10 @@ def main() -> int:
     _log(f"whole call: {ms_step * 1e3:.1f} us/call (wall {wall / args.steps * 1e6:.1f} us/call)")
 
     # the dominant kernel alone: the decode pass (partials when split)
-    if splits > 1:
+    if flat:
+        fo, fl = _WS.get_flat(wl.batch + flat, shape.num_q_heads, shape.head_dim, dev)
+        run = lambda c: decode_partials(q, c, 1, part_out=fo, part_lse=fl, flat_splits=flat, out=out)
+    elif splits > 1:
         part_out, part_lse = _WS.get(wl.batch, shape.num_q_heads, splits, shape.head_dim, dev)
         run = lambda c: decode_partials(q, c, splits, part_out=part_out, part_lse=part_lse,
                                          max_seq_len=msl)
@@ -398,6 +412,7 @@ def main() -> int:
             "block_size": 16,
             "seq_len_max": max(wl.lens),
             "num_splits": splits,
+            "flat_splits": flat,
             "pool_copies_rotated": copies,
             "parallelism": "single GPU",
         },

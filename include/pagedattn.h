@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define PA_ABI_VERSION 2
+#define PA_ABI_VERSION 3
 
 /* Return codes. */
 #define PA_OK 0
@@ -76,8 +76,10 @@ extern "C" {
 #define PA_IO_FP16 0
 #define PA_IO_BF16 1
 
-/* Largest supported split count and GQA group handled in one pass. */
+/* Largest supported split count, flat split count and GQA group handled in
+ * one pass. */
 #define PA_MAX_SPLITS 4096
+#define PA_MAX_FLAT_SPLITS 65536
 #define PA_MAX_GROUP 16
 
 typedef struct pa_decode_args {
@@ -122,6 +124,16 @@ typedef struct pa_decode_args {
   int32_t scale_dtype; /* PA_SCALE_* */
   int32_t io_dtype;    /* PA_IO_* */
   float sm_scale;      /* softmax scale applied to q.k (natural-log domain) */
+  /* Flat (work-balanced) split, an addition with no counterpart in the
+   * reference. 0: off (num_splits decides). F > 0: per (kv head, 16-head
+   * tile), the batch's 32-token tiles are concatenated in sequence order and
+   * cut into F equal contiguous ranges, one wave each, so every wave streams
+   * the same number of tiles however ragged seq_lens is; num_splits and
+   * max_seq_len are ignored. Workspace: part_out [batch + F, num_q_heads,
+   * head_dim] with stride_pb / stride_ph (slot, head) and part_lse
+   * [batch + F, num_q_heads] with stride_lb / stride_lh; stride_ps is unused.
+   * Every wave scans seq_lens once (batch / 64 loads per lane). */
+  int32_t flat_splits;
 } pa_decode_args;
 
 typedef struct pa_reduce_args {
@@ -148,12 +160,17 @@ typedef struct pa_reduce_args {
  * that fits in one split is written to `out` by the decode kernel and skipped
  * by the merge, and the merge reads a sequence's non-empty splits only. (So
  * part_out / part_lse are scratch here; pa_decode_partials fills them all.)
+ * flat_splits > 0: the flat decode kernel writes a sequence held by one
+ * wave range to `out` and the others as partial slots, then the merge
+ * kernel folds each sequence's slots (see pa_decode_args.flat_splits).
  * A sequence with T_b == 0 yields zeros (the reference yields NaN there).
  * Replaces pagedattn/triton_decode.py:331-376. */
 int pa_decode(const pa_decode_args *args, void *stream);
 
 /* Decode pass only: writes part_out / part_lse (num_splits >= 1) and skips
  * the merge, so a caller can time or distribute the passes separately.
+ * With flat_splits > 0 it is the flat decode pass alone: partial slots, and
+ * `out` for the sequences that one range holds whole.
  * Replaces the `_paged_decode_kernel[(b, hkv, num_splits)]` launch
  * (pagedattn/triton_decode.py:351-367). */
 int pa_decode_partials(const pa_decode_args *args, void *stream);
@@ -196,6 +213,15 @@ typedef struct pa_cache_write_args {
  * `reshape_and_cache_flash` at integration/vllm_backend.py:117-122 for
  * caches in this library's formats. */
 int pa_cache_write(const pa_cache_write_args *args, void *stream);
+
+/* Workgroups of the flat decode kernel for (kv_dtype, scale_dtype,
+ * head_dim) that one CU holds at once (hipOccupancyMaxActiveBlocksPerMultiprocessor
+ * on the current device), written to *out. A host planner sizes
+ * flat_splits from it: one round of resident waves is
+ * CUs * 4 * (*out) waves over num_kv_heads * ceil(group / 16) units.
+ * No counterpart in the reference (its split count comes from the SM count
+ * alone, pagedattn/triton_decode.py:248-263). */
+int pa_flat_workgroups_per_cu(int kv_dtype, int scale_dtype, int head_dim, int *out);
 
 /* Message for the last non-zero return on the calling thread ("" if none). */
 const char *pa_last_error(void);

@@ -197,6 +197,72 @@ def split_partials(
     return part, lse
 
 
+def flat_segments(seq_lens, flat_splits: int, align: int = 32) -> tuple[list[tuple[int, int, int, int]], int]:
+    """The flat split's work list and range size: ([(j, b, lo, hi)], per).
+
+    No counterpart in the reference: the HIP build's work-balanced split.
+    Sequence b owns flat tiles [cu_b, cu_b + n_b), n_b = ceil(T_b / align),
+    in batch order; range j covers flat tiles [j * per, (j + 1) * per) with
+    per = max(1, ceil(total / flat_splits)). Each (j, b, lo, hi) is the token
+    range [lo, hi) of sequence b that range j holds, in order.
+    """
+    lens = [max(0, int(t)) for t in seq_lens]
+    tiles = [-(-t // align) for t in lens]
+    total = sum(tiles)
+    per = max(1, -(-total // flat_splits))
+    segs = []
+    cu = 0
+    for b, (t, n) in enumerate(zip(lens, tiles)):
+        f = cu
+        while f < cu + n:
+            j = f // per
+            end = min(cu + n, (j + 1) * per)
+            segs.append((j, b, (f - cu) * align, min((end - cu) * align, t)))
+            f = end
+        cu += n
+    return segs, per
+
+
+def flat_partials(
+    q: torch.Tensor,
+    cache,
+    flat_splits: int,
+    align: int = 32,
+    sm_scale: float | None = None,
+) -> tuple[torch.Tensor, torch.Tensor, list[bool]]:
+    """The flat decode pass: (part [B + F, Hq, D], lse [B + F, Hq], whole [B]).
+
+    Slot b + j holds the normalised output and log2-sum-exp (as in
+    split_partials) of the segment of sequence b in range j; whole[b] is True
+    when one range holds all of b (the decode then writes `out` instead of a
+    slot). Unused slots stay (0, -inf).
+    """
+    qc = q.cpu().float()
+    b, hq, d = qc.shape
+    group = hq // cache.shape.num_kv_heads
+    k, v = gather_contiguous(cache)
+    k = k.float()
+    v = v.float()
+    scale = _softmax_scale(cache, sm_scale) * math.log2(math.e)
+    lens = cache.seq_lens.cpu().long().tolist()
+    segs, _ = flat_segments(lens, flat_splits, align)
+    part = torch.zeros((b + flat_splits, hq, d), dtype=torch.float32)
+    lse = torch.full((b + flat_splits, hq), float("-inf"), dtype=torch.float32)
+    count = [0] * b
+    for _, bi, _, _ in segs:
+        count[bi] += 1
+    for j, bi, lo, hi in segs:
+        for h in range(hq):
+            kvh = h // group
+            x = (k[bi, kvh, lo:hi] @ qc[bi, h]) * scale
+            m = x.max()
+            w = torch.exp2(x - m)
+            den = w.sum()
+            part[bi + j, h] = (w @ v[bi, kvh, lo:hi]) / den
+            lse[bi + j, h] = m + torch.log2(den)
+    return part, lse, [c == 1 for c in count]
+
+
 def split_merge(part: torch.Tensor, lse: torch.Tensor) -> torch.Tensor:
     """out = sum_s part_s 2^(lse_s - m) / sum_s 2^(lse_s - m). triton_decode.py:221-240.
     Returns fp32 [B, H, D]; rows whose splits are all empty give NaN (0/0),

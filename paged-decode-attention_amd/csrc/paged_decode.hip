@@ -49,6 +49,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <type_traits>
+
 #include "pagedattn.h"
 #include "pa_errors.h"
 
@@ -78,6 +80,8 @@ struct KParams {
   const int32_t *bt;
   const int32_t *seq_lens;
   int32_t hkv, group, head_tiles, num_splits, num_blocks, max_blocks, log2_page, max_seq_len;
+  int32_t batch, max_tokens;  // max_tokens = max_blocks << log2_page
+  int32_t flat_splits;        // > 0: the flat (work-balanced) split
   int64_t sqb, sqh;          // elements
   int64_t skn, skt, skh;     // bytes
   int64_t ssn, sst;          // bytes
@@ -94,9 +98,10 @@ struct RParams {
   const float *part_lse;
   uint8_t *out;
   int32_t io_bf16;  // out is bf16 (else fp16)
-  const int32_t *seq_lens;  // AUTO merge only
-  int32_t max_tokens, max_seq_len;  // AUTO merge only
-  int32_t num_heads, num_splits;
+  const int32_t *seq_lens;  // AUTO and FLAT merges only
+  int32_t max_tokens, max_seq_len;  // AUTO and FLAT merges only
+  int32_t num_heads, num_splits;    // FLAT: num_splits = flat splits
+  int32_t batch;                    // FLAT only
   int64_t spb, sph, sps, slb, slh, sob, soh;  // elements
 };
 
@@ -515,6 +520,136 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
   }
 }
 
+// Q^T B-operands of query heads qh0 .. qh0 + nh - 1 of sequence b (lane
+// column r16 = head, padded columns are zero).
+template <int KV, int D>
+__device__ __forceinline__ void load_q(WaveState<KV, D> &st, const KParams &p, int b, int qh0,
+                                       int nh, int r16, int c) {
+  using G = Geo<KV, D>;
+  const bool hv = r16 < nh;
+  const uint16_t *qrow = reinterpret_cast<const uint16_t *>(p.q) + (int64_t)b * p.sqb +
+                         (int64_t)(qh0 + (hv ? r16 : 0)) * p.sqh;
+#pragma unroll
+  for (int ks = 0; ks < G::kKSteps; ++ks) {
+    f16x8 qv = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (hv) {
+      const u32x4 w = *reinterpret_cast<const u32x4 *>(qrow + 32 * ks + 8 * c);
+      qv = p.io_bf16 ? bf16x8_to_f16x8(w) : __builtin_bit_cast(f16x8, w);
+    }
+    st.qop[ks] = qv;
+  }
+}
+
+template <int KV, int D>
+__device__ __forceinline__ void reset_state(WaveState<KV, D> &st) {
+  using G = Geo<KV, D>;
+  st.m = -INFINITY;
+  st.l = 0.f;
+#pragma unroll
+  for (int sl = 0; sl < G::kE; ++sl) st.acc[sl] = f32x4{0.f, 0.f, 0.f, 0.f};
+}
+
+// One lane's share of a finished row of head h: y[0 .. 4*kE) = O[h][d0 ..)
+// (already normalised), L the row's sum of 2^(s - M). Written to `out` of
+// sequence b (direct) or as a partial row at element offsets part_off /
+// lse_off (the lse by the c == 0 lane).
+template <int D>
+__device__ __forceinline__ void store_result(const KParams &p, const float *y, float L, float M,
+                                             int b, int h, int d0, int c, bool direct,
+                                             int64_t part_off, int64_t lse_off) {
+  constexpr int kRegs = 4 * (D / 16);
+  if (!direct) {
+    float *dst = p.part_out + part_off + (int64_t)h * p.sph + d0;
+#pragma unroll
+    for (int v4 = 0; v4 < kRegs / 4; ++v4) {
+      f32x4 t4 = {y[4 * v4], y[4 * v4 + 1], y[4 * v4 + 2], y[4 * v4 + 3]};
+      *reinterpret_cast<f32x4 *>(dst + 4 * v4) = t4;
+    }
+    if (c == 0) p.part_lse[lse_off + (int64_t)h * p.slh] = (L > 0.f) ? M + __log2f(L) : -INFINITY;
+  } else {
+    uint8_t *dst = p.out + ((int64_t)b * p.sob + (int64_t)h * p.soh + d0) * 2;
+    if (p.io_bf16) {
+      uint32_t w[kRegs / 2];
+#pragma unroll
+      for (int e = 0; e < kRegs / 2; ++e)
+        w[e] = f32_to_bf16_bits(y[2 * e]) | (f32_to_bf16_bits(y[2 * e + 1]) << 16);
+#pragma unroll
+      for (int e = 0; e < kRegs / 2; e += 2)
+        *reinterpret_cast<u32x2 *>(dst + 4 * e) = u32x2{w[e], w[e + 1]};
+    } else if constexpr (kRegs >= 8) {
+#pragma unroll
+      for (int v8 = 0; v8 < kRegs / 8; ++v8) {
+        f16x8 t8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) t8[e] = (_Float16)y[8 * v8 + e];
+        *reinterpret_cast<f16x8 *>(dst + 16 * v8) = t8;
+      }
+    } else {
+      store_row(dst, y, kRegs, false);
+    }
+  }
+}
+
+// The same result written straight from the accumulators, a few registers at
+// a time: acc[sl][i] (sl = 0 .. kE-1) are the kE contiguous head-dim elements
+// from 4*kE*c + kE*i, scaled by `inv` on the way out.
+template <int D>
+__device__ __forceinline__ void store_acc(const KParams &p, const f32x4 *acc, float inv, float L,
+                                          float M, int b, int h, int c, bool direct,
+                                          int64_t part_off, int64_t lse_off) {
+  constexpr int kE = D / 16;
+  const int d0 = 4 * kE * c;
+  if (!direct) {
+    float *dst = p.part_out + part_off + (int64_t)h * p.sph + d0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (kE >= 4) {
+#pragma unroll
+        for (int q = 0; q < kE / 4; ++q) {
+          const f32x4 t4 = {acc[4 * q][i] * inv, acc[4 * q + 1][i] * inv, acc[4 * q + 2][i] * inv,
+                            acc[4 * q + 3][i] * inv};
+          *reinterpret_cast<f32x4 *>(dst + kE * i + 4 * q) = t4;
+        }
+      } else {
+#pragma unroll
+        for (int sl = 0; sl < kE; ++sl) dst[kE * i + sl] = acc[sl][i] * inv;
+      }
+    }
+    if (c == 0) p.part_lse[lse_off + (int64_t)h * p.slh] = (L > 0.f) ? M + __log2f(L) : -INFINITY;
+  } else {
+    // kE (even) elements of group i = kE / 2 dwords at byte offset 2 * kE * i
+    uint32_t *dst = reinterpret_cast<uint32_t *>(
+        p.out + ((int64_t)b * p.sob + (int64_t)h * p.soh + d0) * 2);
+    if (p.io_bf16) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < kE; e += 2)
+          dst[(kE * i + e) / 2] =
+              f32_to_bf16_bits(acc[e][i] * inv) | (f32_to_bf16_bits(acc[e + 1][i] * inv) << 16);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < kE; e += 2) {
+          const f16x2 hh = {(_Float16)(acc[e][i] * inv), (_Float16)(acc[e + 1][i] * inv)};
+          dst[(kE * i + e) / 2] = __builtin_bit_cast(uint32_t, hh);
+        }
+    }
+  }
+}
+
+// Lane (c, h) holds O[h][4*kE*c + kE*i + sl] in acc[sl][i]; regroup so that
+// y[kE*i + sl] is head-dim offset 4*kE*c + kE*i + sl (contiguous), scaled.
+template <int D>
+__device__ __forceinline__ void regroup(float *y, const float *o, float scale) {
+  constexpr int kE = D / 16;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int sl = 0; sl < kE; ++sl) y[kE * i + sl] = o[4 * sl + i] * scale;
+}
+
 // Token range [lo, hi) of one split, and how many of the sequence's splits
 // hold tokens. chunk = ceil(ceil(T / 32) / S) * 32 tokens, T = the sequence's
 // length (the reference's per-sequence rule, triton_decode.py:78-85), or the
@@ -611,24 +746,8 @@ paged_decode_kernel(const KParams p) {
   }
 
   WaveState<KV, D> st;
-  st.m = -INFINITY;
-  st.l = 0.f;
-#pragma unroll
-  for (int sl = 0; sl < G::kE; ++sl) st.acc[sl] = f32x4{0.f, 0.f, 0.f, 0.f};
-  {
-    const bool hv = r16 < nh;
-    const uint16_t *qrow = reinterpret_cast<const uint16_t *>(p.q) + (int64_t)b * p.sqb +
-                           (int64_t)(qh0 + (hv ? r16 : 0)) * p.sqh;
-#pragma unroll
-    for (int ks = 0; ks < G::kKSteps; ++ks) {
-      f16x8 qv = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (hv) {
-        const u32x4 w = *reinterpret_cast<const u32x4 *>(qrow + 32 * ks + 8 * c);
-        qv = p.io_bf16 ? bf16x8_to_f16x8(w) : __builtin_bit_cast(f16x8, w);
-      }
-      st.qop[ks] = qv;
-    }
-  }
+  reset_state(st);
+  load_q(st, p, b, qh0, nh, r16, c);
 
   const int32_t *bt_row = p.bt + (int64_t)b * p.sbtb;
   float *sc_lds = sm_sc[wave];
@@ -701,49 +820,215 @@ paged_decode_kernel(const KParams p) {
       o[4 * sl + i] = a;
     }
   const float inv = (L > 0.f) ? 1.0f / L : 0.f;
-
-  // Lane (c, h) holds O[h][4*kE*c + kE*i + sl] in o[4*sl + i]; regroup so that
-  // y[kE*i + sl] is head-dim offset 4*kE*c + kE*i + sl (contiguous).
   float y[kRegs];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int sl = 0; sl < G::kE; ++sl) y[G::kE * i + sl] = o[4 * sl + i] * inv;
-
+  regroup<D>(y, o, inv);
   if (r16 >= nh) return;
-  const int h = qh0 + r16;
-  const int d0 = 4 * G::kE * c;
-  if (!direct) {
-    float *dst = p.part_out + (int64_t)b * p.spb + (int64_t)h * p.sph + (int64_t)split * p.sps + d0;
+  store_result<D>(p, y, L, M, b, qh0 + r16, 4 * G::kE * c, c, direct,
+                  (int64_t)b * p.spb + (int64_t)split * p.sps, (int64_t)b * p.slb + split);
+}
+
+// ----------------------------------------------------------------------------
+// Flat (work-balanced) split.
+//
+// Per (kv_head, head_tile) unit, the batch's 32-token tiles are laid end to
+// end in sequence order: sequence b owns flat tiles [cu_b, cu_b + n_b),
+// n_b = ceil(T_b / 32). The F = flat_splits waves of the unit take F equal
+// contiguous ranges of per = ceil(total / F) tiles, so every wave streams the
+// same number of tiles however ragged the lengths are (the classic split gives
+// each sequence its own chunks, and a few long sequences then run alone at the
+// end of the launch). A wave keeps the tile pipeline going across sequence
+// boundaries; when its range leaves a sequence it writes that segment's
+// normalised output and log2-sum-exp as partial slot b + j (j = the wave's
+// range index), or `out` itself when the segment is the whole sequence.
+// Slots are unique: if range j - 1 reached sequence b + 1, sequence b ended
+// before range j began. The merge (split_reduce_kernel<D, kFlatMerge>)
+// derives the same ranges from seq_lens and folds slots b + j0 .. b + j1.
+// ----------------------------------------------------------------------------
+
+// Tiles of sequence b (its length clamped to the block table).
+__device__ __forceinline__ int seq_tiles(const int32_t *seq_lens, int b, int max_tokens) {
+  const int t = max(0, min(seq_lens[b], max_tokens));
+  return (t + kSplitAlign - 1) / kSplitAlign;
+}
+
+__device__ __forceinline__ int wave_sum(int x) {
 #pragma unroll
-    for (int v4 = 0; v4 < kRegs / 4; ++v4) {
-      f32x4 t4 = {y[4 * v4], y[4 * v4 + 1], y[4 * v4 + 2], y[4 * v4 + 3]};
-      *reinterpret_cast<f32x4 *>(dst + 4 * v4) = t4;
+  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+__device__ __forceinline__ int wave_incl_scan(int x, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+
+// Total flat tiles of the batch (wave-uniform).
+__device__ __forceinline__ int flat_total(const int32_t *seq_lens, int batch, int max_tokens,
+                                          int lane) {
+  int total = 0;
+  for (int base = 0; base < batch; base += 64) {
+    const int b = base + lane;
+    total += wave_sum(b < batch ? seq_tiles(seq_lens, b, max_tokens) : 0);
+  }
+  return __builtin_amdgcn_readfirstlane(total);
+}
+
+// A wave's position in its range: sequence b, tile t of b, b's tile count
+// and length (all wave-uniform).
+struct SeqCursor {
+  int b, t, tiles, len;
+};
+
+// The sequence holding flat tile f (< total) and f's tile index in it.
+__device__ __forceinline__ SeqCursor flat_locate(const int32_t *seq_lens, int batch, int max_tokens,
+                                                 int f, int lane) {
+  SeqCursor cur = {0, 0, 0, 0};
+  int run = 0;
+  for (int base = 0; base < batch; base += 64) {
+    const int b = base + lane;
+    const int t = b < batch ? seq_tiles(seq_lens, b, max_tokens) : 0;
+    const int incl = wave_incl_scan(t, lane) + run;
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(incl > f);
+    if (hit != 0) {
+      const int l = __builtin_ctzll(hit);
+      cur.b = base + l;
+      cur.t = f - __shfl(incl - t, l);
+      break;
     }
-    if (c == 0) {
-      p.part_lse[(int64_t)b * p.slb + (int64_t)h * p.slh + split] =
-          (L > 0.f) ? M + __log2f(L) : -INFINITY;
-    }
-  } else {
-    uint8_t *dst = p.out + ((int64_t)b * p.sob + (int64_t)h * p.soh + d0) * 2;
-    if (p.io_bf16) {
-      uint32_t w[kRegs / 2];
-#pragma unroll
-      for (int e = 0; e < kRegs / 2; ++e)
-        w[e] = f32_to_bf16_bits(y[2 * e]) | (f32_to_bf16_bits(y[2 * e + 1]) << 16);
-#pragma unroll
-      for (int e = 0; e < kRegs / 2; e += 2)
-        *reinterpret_cast<u32x2 *>(dst + 4 * e) = u32x2{w[e], w[e + 1]};
-    } else if constexpr (kRegs >= 8) {
-#pragma unroll
-      for (int v8 = 0; v8 < kRegs / 8; ++v8) {
-        f16x8 t8;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) t8[e] = (_Float16)y[8 * v8 + e];
-        *reinterpret_cast<f16x8 *>(dst + 16 * v8) = t8;
+    run = __shfl(incl, 63);
+  }
+  cur.b = __builtin_amdgcn_readfirstlane(cur.b);
+  cur.t = __builtin_amdgcn_readfirstlane(cur.t);
+  cur.len = __builtin_amdgcn_readfirstlane(max(0, min(seq_lens[cur.b], max_tokens)));
+  cur.tiles = (cur.len + kSplitAlign - 1) / kSplitAlign;
+  return cur;
+}
+
+// Step to the next flat tile. Only called while the range has another tile,
+// so a non-empty sequence follows; the batch bound only guards the reads.
+__device__ __forceinline__ void cursor_next(SeqCursor &cur, const int32_t *seq_lens, int batch,
+                                            int max_tokens) {
+  if (++cur.t < cur.tiles) return;
+  cur.t = 0;
+  while (cur.b + 1 < batch) {
+    ++cur.b;
+    cur.len = __builtin_amdgcn_readfirstlane(max(0, min(seq_lens[cur.b], max_tokens)));
+    cur.tiles = (cur.len + kSplitAlign - 1) / kSplitAlign;
+    if (cur.tiles > 0) break;
+  }
+}
+
+// 1-byte KV at head_dim <= 128 fits three workgroups per CU.
+template <int KV, int SC, int D>
+__global__ void __launch_bounds__(kWaves * 64)
+__attribute__((amdgpu_waves_per_eu(Geo<KV, D>::kElem == 1 && D <= 128 ? 3 : 2)))
+paged_decode_flat_kernel(const KParams p) {
+  using G = Geo<KV, D>;
+  static_assert(G::kTT == kSplitAlign, "flat tiles are the kernel's tiles");
+  __shared__ __attribute__((aligned(16))) uint8_t sm_k[kWaves * G::kKSlotBytes];
+  __shared__ __attribute__((aligned(16))) float sm_sc[kWaves][G::kScales];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15;
+  const int c = lane >> 4;
+
+  // XCD-contiguous workgroup order, as for the classic split launch: an XCD
+  // holds neighbouring ranges, i.e. a contiguous stretch of the batch.
+  int wg = blockIdx.x;
+  {
+    const int n = gridDim.x, full = n - n % 8;
+    if (wg < full) wg = (wg % 8) * (full / 8) + wg / 8;
+  }
+  // global wave = j * units + unit: the waves of a workgroup share a range
+  // and cover neighbouring kv heads, which read the same pages.
+  const int units = p.hkv * p.head_tiles;
+  const int gw = wg * kWaves + wave;
+  if (gw >= units * p.flat_splits) return;  // no barrier follows: waves are independent
+  const int unit = gw % units;
+  const int j = gw / units;
+  const int kvh = unit / p.head_tiles;
+  const int ht = unit % p.head_tiles;
+  const int qh0 = kvh * p.group + ht * 16;
+  const int nh = min(16, p.group - ht * 16);
+
+  const int total = flat_total(p.seq_lens, p.batch, p.max_tokens, lane);
+  const int per = max(1, (total + p.flat_splits - 1) / p.flat_splits);
+  const int r0 = j * per;
+  if (r0 >= total) return;
+  const int n = min(per, total - r0);  // this wave's tiles
+
+  SeqCursor cc = flat_locate(p.seq_lens, p.batch, p.max_tokens, r0, lane);  // compute cursor
+  SeqCursor lc = cc;                                                        // load cursor
+  int seg_t0 = cc.t;  // first tile of the current segment
+
+  WaveState<KV, D> st;
+  reset_state(st);
+  load_q(st, p, cc.b, qh0, nh, r16, c);
+
+  float *sc_lds = sm_sc[wave];
+  uint8_t *k_lds = sm_k + wave * G::kKSlotBytes;
+
+  auto bt_of = [&](int b) { return p.bt + (int64_t)b * p.sbtb; };
+  // After computing the wave's i-th tile: close the segment at a sequence
+  // end or at the end of the range, then move the compute cursor on.
+  auto post = [&](int i) {
+    const bool seq_end = cc.t + 1 == cc.tiles;
+    if (seq_end || i + 1 == n) {
+      const float L = col_sum(st.l);
+      const float inv = (L > 0.f) ? 1.0f / L : 0.f;
+      if (r16 < nh) {
+        const int slot = cc.b + j;
+        store_acc<D>(p, st.acc, inv, L, st.m, cc.b, qh0 + r16, c, seg_t0 == 0 && seq_end,
+                     (int64_t)slot * p.spb, (int64_t)slot * p.slb);
+      }
+      if (i + 1 < n) {
+        cursor_next(cc, p.seq_lens, p.batch, p.max_tokens);
+        seg_t0 = 0;
+        reset_state(st);
+        load_q(st, p, cc.b, qh0, nh, r16, c);
       }
     } else {
-      store_row(dst, y, kRegs, false);
+      ++cc.t;
+    }
+  };
+  auto n0_of = [](const SeqCursor &cur) { return cur.t * G::kTT; };
+
+  if constexpr (G::kPrefetch) {
+    Tile<KV, D> ta, tb;
+    load_tile<KV, SC, D>(ta, p, bt_of(lc.b), kvh, n0_of(lc), lc.len, lane);
+    int i = 0;
+    for (; i + 2 < n; i += 2) {
+      cursor_next(lc, p.seq_lens, p.batch, p.max_tokens);
+      load_tile<KV, SC, D>(tb, p, bt_of(lc.b), kvh, n0_of(lc), lc.len, lane);
+      compute_tile<KV, SC, D>(st, ta, p, n0_of(cc), cc.len, lane, sc_lds, k_lds);
+      post(i);
+      cursor_next(lc, p.seq_lens, p.batch, p.max_tokens);
+      load_tile<KV, SC, D>(ta, p, bt_of(lc.b), kvh, n0_of(lc), lc.len, lane);
+      compute_tile<KV, SC, D>(st, tb, p, n0_of(cc), cc.len, lane, sc_lds, k_lds);
+      post(i + 1);
+    }
+    if (i + 1 < n) {
+      cursor_next(lc, p.seq_lens, p.batch, p.max_tokens);
+      load_tile<KV, SC, D>(tb, p, bt_of(lc.b), kvh, n0_of(lc), lc.len, lane);
+      compute_tile<KV, SC, D>(st, ta, p, n0_of(cc), cc.len, lane, sc_lds, k_lds);
+      post(i);
+      compute_tile<KV, SC, D>(st, tb, p, n0_of(cc), cc.len, lane, sc_lds, k_lds);
+      post(i + 1);
+    } else {
+      compute_tile<KV, SC, D>(st, ta, p, n0_of(cc), cc.len, lane, sc_lds, k_lds);
+      post(i);
+    }
+  } else {
+    for (int i = 0; i < n; ++i) {
+      Tile<KV, D> t;
+      load_tile<KV, SC, D>(t, p, bt_of(cc.b), kvh, n0_of(cc), cc.len, lane);
+      compute_tile<KV, SC, D>(st, t, p, n0_of(cc), cc.len, lane, sc_lds, k_lds);
+      post(i);
     }
   }
 }
@@ -754,9 +1039,38 @@ paged_decode_kernel(const KParams p) {
 // loads in flight, so repeated calls are bit-identical.
 constexpr int kReduceChunk = 256;  // splits whose weights are staged at once
 
-// AUTO: the partials of a kAuto decode; only the sequence's non-empty splits
-// are read, and sequences held by one split (already written) are skipped.
-template <int D, bool AUTO>
+// Store one lane's slice of a merged row: acc / wsum (zeros when wsum is 0).
+template <int D>
+__device__ __forceinline__ void write_merged(const RParams &p, const float *acc, float wsum, int b,
+                                             int h, int lane, bool active) {
+  constexpr int kPer = D / 64 > 0 ? D / 64 : 1;
+  const float inv = (wsum > 0.f) ? 1.0f / wsum : 0.f;
+  if (!active) return;
+  uint8_t *dst = p.out + ((int64_t)b * p.sob + (int64_t)h * p.soh + lane * kPer) * 2;
+  float y[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) y[i] = acc[i] * inv;
+  if constexpr (kPer >= 2) {
+    store_row(dst, y, kPer, p.io_bf16 != 0);
+  } else {
+    const uint16_t bits = p.io_bf16 ? (uint16_t)f32_to_bf16_bits(y[0])
+                                    : __builtin_bit_cast(uint16_t, (_Float16)y[0]);
+    *reinterpret_cast<uint16_t *>(dst) = bits;
+  }
+}
+
+// What the merge reads:
+//   kMergeAll   every split of [B, H, S] partials (pa_split_reduce)
+//   kMergeAuto  the partials of a kAuto decode: only the sequence's non-empty
+//               splits; sequences held by one split (already written) are
+//               skipped
+//   kMergeFlat  the slots of a flat decode: sequence b's partials are slots
+//               b + j0 .. b + j1 for the ranges j0 .. j1 that cut it;
+//               sequences inside one range (already written) are skipped and
+//               empty sequences get zeros
+enum { kMergeAll = 0, kMergeAuto = 1, kMergeFlat = 2 };
+
+template <int D, int KIND>
 __global__ void __launch_bounds__(64) split_reduce_kernel(const RParams p) {
   constexpr int kPer = D / 64 > 0 ? D / 64 : 1;  // head-dim elements per lane
   __shared__ float sw[kReduceChunk];
@@ -766,42 +1080,101 @@ __global__ void __launch_bounds__(64) split_reduce_kernel(const RParams p) {
   const int h = bh % p.num_heads;
   const float *lse = p.part_lse + (int64_t)b * p.slb + (int64_t)h * p.slh;
   const float *part = p.part_out + (int64_t)b * p.spb + (int64_t)h * p.sph;
+  int64_t lse_step = 1;   // elements between consecutive partials
+  int64_t part_step = p.sps;
   int S = p.num_splits;
-  if (AUTO) {
+  if (KIND == kMergeAuto) {
     const int seq_len = max(0, min(p.seq_lens[b], p.max_tokens));
     S = split_range(seq_len, p.num_splits, p.max_seq_len, 0).n;
     if (S <= 1) return;
+  } else if (KIND == kMergeFlat) {
+    // the decode's ranges: per = ceil(total / F) flat tiles each
+    int total = 0, cu = 0;
+    for (int base = 0; base < p.batch; base += 64) {
+      const int bb = base + lane;
+      const int t = bb < p.batch ? seq_tiles(p.seq_lens, bb, p.max_tokens) : 0;
+      total += wave_sum(t);
+      cu += wave_sum(bb < b ? t : 0);
+    }
+    const int nt = seq_tiles(p.seq_lens, b, p.max_tokens);
+    S = 0;  // empty sequence: the merge below writes zeros
+    if (nt > 0) {
+      const int per = max(1, (total + p.num_splits - 1) / p.num_splits);
+      const int j0 = cu / per, j1 = (cu + nt - 1) / per;
+      if (j0 == j1) return;
+      S = j1 - j0 + 1;
+      lse = p.part_lse + (int64_t)(b + j0) * p.slb + (int64_t)h * p.slh;
+      part = p.part_out + (int64_t)(b + j0) * p.spb + (int64_t)h * p.sph;
+      lse_step = p.slb;
+      part_step = p.spb;
+    }
   }
-
-  float m = -INFINITY;
-  for (int s = lane; s < S; s += 64) m = fmaxf(m, lse[s]);
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
 
   const bool active = lane * kPer < D;
   float acc[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) acc[i] = 0.f;
-  float wsum = 0.f;  // lane-local partial sums, combined in a fixed tree below
+  float wsum = 0.f;
+
+  // Few splits (the common case): every lane loads all log2-sum-exps and its
+  // slice of every partial in one round trip and folds them in split order.
+  constexpr int kFast = 64 / kPer;
+  if (S <= kFast) {
+    float ls[kFast], v[kFast][kPer];
+#pragma unroll
+    for (int s = 0; s < kFast; ++s) {
+      ls[s] = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) v[s][i] = 0.f;
+      if (s < S) {
+        ls[s] = lse[s * lse_step];
+        if (active) {
+#pragma unroll
+          for (int i = 0; i < kPer; ++i) v[s][i] = part[(int64_t)s * part_step + lane * kPer + i];
+        }
+      }
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < kFast; ++s) m = fmaxf(m, ls[s]);
+#pragma unroll
+    for (int s = 0; s < kFast; ++s) {
+      if (s < S) {
+        const float w = (ls[s] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ls[s] - m);
+        wsum += w;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) acc[i] += w * v[s][i];
+      }
+    }
+    write_merged<D>(p, acc, active ? wsum : 0.f, b, h, lane, active);
+    return;
+  }
+
+  float m = -INFINITY;
+  for (int s = lane; s < S; s += 64) m = fmaxf(m, lse[s * lse_step]);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+
+  // lane-local partial sums of the weights, combined in a fixed tree below
   for (int s0 = 0; s0 < S; s0 += kReduceChunk) {
     const int n = min(kReduceChunk, S - s0);
     __syncthreads();
     for (int s = lane; s < n; s += 64) {
-      const float ls = lse[s0 + s];
+      const float ls = lse[(s0 + s) * lse_step];
       const float w = (ls == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ls - m);
       sw[s] = w;
       wsum += w;
     }
     __syncthreads();
     if (active && m != -INFINITY) {
-      const float *src = part + (int64_t)s0 * p.sps + lane * kPer;
+      const float *src = part + (int64_t)s0 * part_step + lane * kPer;
       int s = 0;
       for (; s + 8 <= n; s += 8) {
         float v[8][kPer];
 #pragma unroll
         for (int j = 0; j < 8; ++j)
 #pragma unroll
-          for (int i = 0; i < kPer; ++i) v[j][i] = src[(int64_t)(s + j) * p.sps + i];
+          for (int i = 0; i < kPer; ++i) v[j][i] = src[(int64_t)(s + j) * part_step + i];
 #pragma unroll
         for (int j = 0; j < 8; ++j)
 #pragma unroll
@@ -809,25 +1182,12 @@ __global__ void __launch_bounds__(64) split_reduce_kernel(const RParams p) {
       }
       for (; s < n; ++s)
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) acc[i] += sw[s] * src[(int64_t)s * p.sps + i];
+        for (int i = 0; i < kPer; ++i) acc[i] += sw[s] * src[(int64_t)s * part_step + i];
     }
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) wsum += __shfl_xor(wsum, o);
-  const float inv = (wsum > 0.f) ? 1.0f / wsum : 0.f;
-  if (active) {
-    uint8_t *dst = p.out + ((int64_t)b * p.sob + (int64_t)h * p.soh + lane * kPer) * 2;
-    float y[kPer];
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) y[i] = acc[i] * inv;
-    if constexpr (kPer >= 2) {
-      store_row(dst, y, kPer, p.io_bf16 != 0);
-    } else {
-      const uint16_t bits = p.io_bf16 ? (uint16_t)f32_to_bf16_bits(y[0])
-                                      : __builtin_bit_cast(uint16_t, (_Float16)y[0]);
-      *reinterpret_cast<uint16_t *>(dst) = bits;
-    }
-  }
+  write_merged<D>(p, acc, wsum, b, h, lane, active);
 }
 
 // ----------------------------------------------------------------------------
@@ -900,8 +1260,11 @@ int build_params(const pa_decode_args *a, bool need_partials, KParams *kp) {
   } else if (a->scale_dtype != PA_SCALE_NONE) {
     return fail(PA_ERR_INVALID, "scale_dtype must be PA_SCALE_NONE for kv_dtype %d", a->kv_dtype);
   }
+  if (a->flat_splits < 0 || a->flat_splits > PA_MAX_FLAT_SPLITS)
+    return fail(PA_ERR_INVALID, "flat_splits %d not in [0, %d]", a->flat_splits, PA_MAX_FLAT_SPLITS);
+  if (a->flat_splits > 0) need_partials = true;
   if (need_partials && (!a->part_out || !a->part_lse))
-    return fail(PA_ERR_INVALID, "num_splits > 1 needs part_out and part_lse");
+    return fail(PA_ERR_INVALID, "num_splits > 1 / flat_splits > 0 need part_out and part_lse");
 
   const int elem = (a->kv_dtype == PA_KV_FP16 || a->kv_dtype == PA_KV_BF16) ? 2 : 1;
   const int64_t strides[] = {a->stride_qb, a->stride_qh, a->stride_kn, a->stride_kt, a->stride_kh,
@@ -931,6 +1294,14 @@ int build_params(const pa_decode_args *a, bool need_partials, KParams *kp) {
   const int head_tiles = (group + PA_MAX_GROUP - 1) / PA_MAX_GROUP;
   const int64_t grid = (int64_t)a->batch * a->num_kv_heads * head_tiles * a->num_splits;
   if (grid > 0x7fffffff) return fail(PA_ERR_UNSUPPORTED, "grid of %lld workgroups too large", (long long)grid);
+  if (a->flat_splits > 0) {
+    // flat tile counts, range starts and slot indices are 32-bit in the kernel
+    const int64_t seq_tiles_max = ((int64_t)a->max_blocks * a->block_size + kSplitAlign - 1) / kSplitAlign;
+    if ((int64_t)a->batch * seq_tiles_max + a->flat_splits > 0x7fffffff)
+      return fail(PA_ERR_UNSUPPORTED, "batch * max tiles per sequence too large for the flat split");
+    if ((int64_t)a->num_kv_heads * head_tiles * a->flat_splits + kWaves > 0x7fffffff)
+      return fail(PA_ERR_UNSUPPORTED, "flat split grid too large");
+  }
 
   KParams &k = *kp;
   k.q = static_cast<const uint8_t *>(a->q);
@@ -951,6 +1322,9 @@ int build_params(const pa_decode_args *a, bool need_partials, KParams *kp) {
   k.max_blocks = a->max_blocks;
   k.log2_page = ilog2(a->block_size);
   k.max_seq_len = a->max_seq_len;
+  k.batch = a->batch;
+  k.max_tokens = a->max_blocks << k.log2_page;
+  k.flat_splits = a->flat_splits;
   k.sqb = a->stride_qb;
   k.sqh = a->stride_qh;
   k.skn = a->stride_kn * elem;
@@ -972,10 +1346,15 @@ int build_params(const pa_decode_args *a, bool need_partials, KParams *kp) {
   return PA_OK;
 }
 
+// Launch modes beyond the classic kernel's.
+constexpr int kFlat = 3;
+
 template <int KV, int SC, int D>
 hipError_t launch_decode_t(const KParams &k, int grid, int mode, hipStream_t st) {
   const dim3 g(grid), blk(kWaves * 64);
-  if (mode == kAuto) {
+  if (mode == kFlat) {
+    hipLaunchKernelGGL((paged_decode_flat_kernel<KV, SC, D>), g, blk, 0, st, k);
+  } else if (mode == kAuto) {
     hipLaunchKernelGGL((paged_decode_kernel<KV, SC, D, kAuto>), g, blk, 0, st, k);
   } else if (mode == kPartials) {
     hipLaunchKernelGGL((paged_decode_kernel<KV, SC, D, kPartials>), g, blk, 0, st, k);
@@ -996,7 +1375,9 @@ hipError_t launch_decode_d(const KParams &k, int d, int grid, int mode, hipStrea
 }
 
 hipError_t launch_decode(const KParams &k, const pa_decode_args *a, int mode, hipStream_t st) {
-  const int grid = a->batch * a->num_kv_heads * k.head_tiles * a->num_splits;
+  const int grid = mode == kFlat
+                       ? (a->num_kv_heads * k.head_tiles * a->flat_splits + kWaves - 1) / kWaves
+                       : a->batch * a->num_kv_heads * k.head_tiles * a->num_splits;
   const int d = a->head_dim;
   if (a->kv_dtype == PA_KV_FP16) return launch_decode_d<PA_KV_FP16, PA_SCALE_NONE>(k, d, grid, mode, st);
   if (a->kv_dtype == PA_KV_BF16) return launch_decode_d<PA_KV_BF16, PA_SCALE_NONE>(k, d, grid, mode, st);
@@ -1029,6 +1410,7 @@ int check_reduce(const pa_reduce_args *r, RParams *rp) {
   rp->seq_lens = nullptr;
   rp->max_tokens = 0;
   rp->max_seq_len = 0;
+  rp->batch = r->batch;
   rp->num_heads = r->num_heads;
   rp->num_splits = r->num_splits;
   rp->spb = r->stride_pb;
@@ -1041,14 +1423,14 @@ int check_reduce(const pa_reduce_args *r, RParams *rp) {
   return PA_OK;
 }
 
-template <bool AUTO>
+template <int KIND>
 hipError_t launch_reduce(const RParams &rp, int batch, int d, hipStream_t st) {
   const int grid = batch * rp.num_heads;
   switch (d) {
-    case 32: hipLaunchKernelGGL((split_reduce_kernel<32, AUTO>), dim3(grid), dim3(64), 0, st, rp); break;
-    case 64: hipLaunchKernelGGL((split_reduce_kernel<64, AUTO>), dim3(grid), dim3(64), 0, st, rp); break;
-    case 128: hipLaunchKernelGGL((split_reduce_kernel<128, AUTO>), dim3(grid), dim3(64), 0, st, rp); break;
-    default: hipLaunchKernelGGL((split_reduce_kernel<256, AUTO>), dim3(grid), dim3(64), 0, st, rp); break;
+    case 32: hipLaunchKernelGGL((split_reduce_kernel<32, KIND>), dim3(grid), dim3(64), 0, st, rp); break;
+    case 64: hipLaunchKernelGGL((split_reduce_kernel<64, KIND>), dim3(grid), dim3(64), 0, st, rp); break;
+    case 128: hipLaunchKernelGGL((split_reduce_kernel<128, KIND>), dim3(grid), dim3(64), 0, st, rp); break;
+    default: hipLaunchKernelGGL((split_reduce_kernel<256, KIND>), dim3(grid), dim3(64), 0, st, rp); break;
   }
   return hipGetLastError();
 }
@@ -1102,25 +1484,29 @@ const char *pa_last_error(void) { return g_err; }
 
 int pa_decode(const pa_decode_args *a, void *stream) {
   KParams k;
-  const bool split = a != nullptr && a->num_splits > 1;
+  const bool flat = a != nullptr && a->flat_splits > 0;
+  const bool split = a != nullptr && (a->num_splits > 1 || flat);
   int rc = build_params(a, split, &k);
   if (rc != PA_OK) return rc;
   RParams rp;
   pa_reduce_args ra;
   if (split) {
     ra = reduce_args_from(a);
+    if (flat) ra.num_splits = 1;  // validated above; the merge reads flat_splits
     rc = check_reduce(&ra, &rp);
     if (rc != PA_OK) return rc;
     rp.seq_lens = a->seq_lens;
-    rp.max_tokens = k.max_blocks << k.log2_page;
+    rp.max_tokens = k.max_tokens;
     rp.max_seq_len = a->max_seq_len;
+    if (flat) rp.num_splits = a->flat_splits;
   }
   if (a->batch == 0) return ok();
   hipStream_t st = static_cast<hipStream_t>(stream);
-  hipError_t e = launch_decode(k, a, split ? kAuto : kUnsplit, st);
+  hipError_t e = launch_decode(k, a, flat ? kFlat : split ? kAuto : kUnsplit, st);
   if (e != hipSuccess) return fail(PA_ERR_HIP, "decode launch failed: %s", hipGetErrorString(e));
   if (split) {
-    e = launch_reduce<true>(rp, a->batch, a->head_dim, st);
+    e = flat ? launch_reduce<kMergeFlat>(rp, a->batch, a->head_dim, st)
+             : launch_reduce<kMergeAuto>(rp, a->batch, a->head_dim, st);
     if (e != hipSuccess) return fail(PA_ERR_HIP, "reduce launch failed: %s", hipGetErrorString(e));
   }
   return ok();
@@ -1131,8 +1517,45 @@ int pa_decode_partials(const pa_decode_args *a, void *stream) {
   int rc = build_params(a, true, &k);
   if (rc != PA_OK) return rc;
   if (a->batch == 0) return ok();
-  hipError_t e = launch_decode(k, a, kPartials, static_cast<hipStream_t>(stream));
+  hipError_t e = launch_decode(k, a, a->flat_splits > 0 ? kFlat : kPartials,
+                               static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(PA_ERR_HIP, "decode launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int pa_flat_workgroups_per_cu(int kv_dtype, int scale_dtype, int head_dim, int *out) {
+  if (out == nullptr) return fail(PA_ERR_INVALID, "out is NULL");
+  *out = 0;
+  if (head_dim != 32 && head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return fail(PA_ERR_UNSUPPORTED, "head_dim %d not in (32, 64, 128, 256)", head_dim);
+  const void *fn = nullptr;
+  auto pick = [&](auto kv_tag, auto sc_tag) {
+    constexpr int KV = decltype(kv_tag)::value, SC = decltype(sc_tag)::value;
+    switch (head_dim) {
+      case 32: fn = reinterpret_cast<const void *>(&paged_decode_flat_kernel<KV, SC, 32>); break;
+      case 64: fn = reinterpret_cast<const void *>(&paged_decode_flat_kernel<KV, SC, 64>); break;
+      case 128: fn = reinterpret_cast<const void *>(&paged_decode_flat_kernel<KV, SC, 128>); break;
+      default: fn = reinterpret_cast<const void *>(&paged_decode_flat_kernel<KV, SC, 256>); break;
+    }
+  };
+  using I = int;
+  if (kv_dtype == PA_KV_FP16 && scale_dtype == PA_SCALE_NONE)
+    pick(std::integral_constant<I, PA_KV_FP16>{}, std::integral_constant<I, PA_SCALE_NONE>{});
+  else if (kv_dtype == PA_KV_BF16 && scale_dtype == PA_SCALE_NONE)
+    pick(std::integral_constant<I, PA_KV_BF16>{}, std::integral_constant<I, PA_SCALE_NONE>{});
+  else if (kv_dtype == PA_KV_FP8_E5M2 && scale_dtype == PA_SCALE_NONE)
+    pick(std::integral_constant<I, PA_KV_FP8_E5M2>{}, std::integral_constant<I, PA_SCALE_NONE>{});
+  else if (kv_dtype == PA_KV_INT8 && scale_dtype == PA_SCALE_FP16)
+    pick(std::integral_constant<I, PA_KV_INT8>{}, std::integral_constant<I, PA_SCALE_FP16>{});
+  else if (kv_dtype == PA_KV_INT8 && scale_dtype == PA_SCALE_FP32)
+    pick(std::integral_constant<I, PA_KV_INT8>{}, std::integral_constant<I, PA_SCALE_FP32>{});
+  else
+    return fail(PA_ERR_INVALID, "kv_dtype %d / scale_dtype %d is not a supported pair", kv_dtype,
+                scale_dtype);
+  int n = 0;
+  const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kWaves * 64, 0);
+  if (e != hipSuccess) return fail(PA_ERR_HIP, "occupancy query failed: %s", hipGetErrorString(e));
+  *out = n;
   return ok();
 }
 
@@ -1141,7 +1564,7 @@ int pa_split_reduce(const pa_reduce_args *r, void *stream) {
   int rc = check_reduce(r, &rp);
   if (rc != PA_OK) return rc;
   if (r->batch == 0) return ok();
-  hipError_t e = launch_reduce<false>(rp, r->batch, r->head_dim, static_cast<hipStream_t>(stream));
+  hipError_t e = launch_reduce<kMergeAll>(rp, r->batch, r->head_dim, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(PA_ERR_HIP, "reduce launch failed: %s", hipGetErrorString(e));
   return ok();
 }

@@ -40,6 +40,12 @@ if str(_PKG_ROOT) not in sys.path:
 
 from pagedattn.cache import PagedKVCache  # noqa: E402
 from pagedattn.config import ModelShape  # noqa: E402
+from pagedattn.hip_decode import (  # noqa: E402
+    MIN_FLAT_TILES_PER_WAVE,
+    TILE_TOKENS,
+    flat_splits_for,
+    flat_workgroups_per_cu,
+)
 from pagedattn.triton_decode import paged_decode_triton, pick_num_splits  # noqa: E402
 
 QUALNAME = "integration.vllm_backend.PagedAttnTritonBackend"
@@ -152,12 +158,21 @@ def decode_forward(impl, layer, query, key, value, kv_cache, attn_metadata, outp
         block_table=attn_metadata.block_table[:n],
         seq_lens=attn_metadata.seq_lens[:n],
     )
-    # max_seq_len is a host int in the metadata, so no device sync here; it
-    # also sizes the split chunks from the longest sequence (ragged balance)
-    splits = pick_num_splits(n, impl.num_kv_heads, int(attn_metadata.max_seq_len),
-                             _cu_count(query.device))
-    decode(query[:n], cache, out=output[:n], num_splits=splits, sm_scale=impl.scale,
-           max_seq_len=int(attn_metadata.max_seq_len))
+    # Host-side only (no device sync): max_seq_len is a host int in the
+    # metadata. The flat split needs no lengths; it is taken when the batch
+    # can hold enough tiles for its waves (the upper bound
+    # n * ceil(max_seq_len / 32) against plan_decode's threshold), otherwise
+    # the classic split, chunked from the longest sequence.
+    msl = int(attn_metadata.max_seq_len)
+    group = impl.num_heads // impl.num_kv_heads
+    flat = flat_splits_for(impl.num_kv_heads, group, _cu_count(query.device),
+                           flat_workgroups_per_cu(cache.kv_dtype, impl.head_size))
+    if n * -(-msl // TILE_TOKENS) >= MIN_FLAT_TILES_PER_WAVE * flat:
+        decode(query[:n], cache, out=output[:n], sm_scale=impl.scale, flat_splits=flat)
+    else:
+        splits = pick_num_splits(n, impl.num_kv_heads, msl, _cu_count(query.device))
+        decode(query[:n], cache, out=output[:n], num_splits=splits, sm_scale=impl.scale,
+               max_seq_len=msl)
     STATS["decode_calls"] += 1
     STATS["decode_tokens"] += n
     return output

@@ -12,9 +12,12 @@ from .cache import PagedKVCache, allocate, quantize_kv
 from .cache_ops import reshape_and_cache
 from .hip_decode import (
     decode_partials,
+    flat_splits_for,
+    flat_workgroups_per_cu,
     paged_decode_hip,
     paged_decode_triton,
     pick_num_splits,
+    plan_decode,
     plan_num_splits,
     split_reduce,
 )
@@ -24,5 +27,6 @@ __all__ = [
     "kv_bytes_per_token",
     "PagedKVCache", "allocate", "quantize_kv", "reshape_and_cache",
     "paged_decode_hip", "paged_decode_triton", "pick_num_splits", "plan_num_splits",
+    "plan_decode", "flat_splits_for", "flat_workgroups_per_cu",
     "decode_partials", "split_reduce",
 ]

@@ -12,7 +12,7 @@ import os
 import pathlib
 import threading
 
-PA_ABI_VERSION = 2
+PA_ABI_VERSION = 3
 
 PA_OK = 0
 PA_ERR_INVALID = -1
@@ -32,6 +32,7 @@ PA_IO_FP16 = 0
 PA_IO_BF16 = 1
 
 PA_MAX_SPLITS = 4096
+PA_MAX_FLAT_SPLITS = 65536
 PA_MAX_GROUP = 16
 
 LIB_NAME = "libpagedattn_hip.so"
@@ -42,6 +43,7 @@ EXPORTED_SYMBOLS = (
     "pa_decode_partials",
     "pa_split_reduce",
     "pa_cache_write",
+    "pa_flat_workgroups_per_cu",
     "pa_last_error",
     "pa_abi_version",
 )
@@ -91,6 +93,7 @@ class PaDecodeArgs(ctypes.Structure):
         ("scale_dtype", _i32),
         ("io_dtype", _i32),
         ("sm_scale", ctypes.c_float),
+        ("flat_splits", _i32),
     ]
 
 
@@ -180,6 +183,9 @@ def load() -> ctypes.CDLL:
         lib.pa_split_reduce.restype = ctypes.c_int
         lib.pa_cache_write.argtypes = [ctypes.POINTER(PaCacheWriteArgs), _vp]
         lib.pa_cache_write.restype = ctypes.c_int
+        lib.pa_flat_workgroups_per_cu.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                                  ctypes.POINTER(ctypes.c_int)]
+        lib.pa_flat_workgroups_per_cu.restype = ctypes.c_int
         lib.pa_last_error.argtypes = []
         lib.pa_last_error.restype = ctypes.c_char_p
         lib.pa_abi_version.argtypes = []

@@ -37,6 +37,17 @@ MIN_SPLIT_TOKENS = 512
 # the BASELINE ragged / long-context shapes: 2 beats 1 and 3).
 SPLIT_ROUNDS = 2
 
+# Flat split: one round of resident waves (a second round measured slower on
+# every BASELINE shape), used when each wave gets at least this many
+# 32-token tiles; below that the batch is too small for it (latency-bound
+# decodes run faster unsplit).
+MIN_FLAT_TILES_PER_WAVE = 4
+# Workgroups of the flat kernel per CU when the library cannot be asked (no
+# GPU): register-limited occupancy of the gfx950 build by (bytes per stored
+# element, head_dim).
+_FLAT_WGS_FALLBACK = {(2, 32): 5, (2, 64): 4, (2, 128): 2, (2, 256): 2,
+                      (1, 32): 5, (1, 64): 4, (1, 128): 3, (1, 256): 2}
+
 _KV_CODE = {"fp16": _abi.PA_KV_FP16, "fp8_e5m2": _abi.PA_KV_FP8_E5M2, "int8": _abi.PA_KV_INT8,
             "bf16": _abi.PA_KV_BF16}
 _STORE_DTYPE = {"fp16": torch.float16, "fp8_e5m2": torch.float8_e5m2, "int8": torch.int8,
@@ -99,6 +110,32 @@ def plan_num_splits(seq_lens, num_kv_heads: int, group: int, sm_count: int) -> t
     return int(splits), tmax
 
 
+def flat_splits_for(num_kv_heads: int, group: int, sm_count: int, workgroups_per_cu: int) -> int:
+    """One round of resident waves over the (kv head, head tile) units."""
+    units = num_kv_heads * -(-group // _abi.PA_MAX_GROUP)
+    waves = max(1, sm_count) * WAVES_PER_WORKGROUP * max(1, workgroups_per_cu)
+    return int(max(1, min(waves // units, _abi.PA_MAX_FLAT_SPLITS)))
+
+
+def plan_decode(seq_lens, num_kv_heads: int, group: int, sm_count: int,
+                workgroups_per_cu: int = 2) -> tuple[int, int, int]:
+    """(num_splits, max_seq_len, flat_splits) for a batch whose lengths the host knows.
+
+    The flat split (one round of resident waves, `flat_splits_for`) whenever
+    each of its waves gets at least MIN_FLAT_TILES_PER_WAVE tiles: it is
+    balanced for any mix of lengths and measured fastest on every BASELINE
+    split shape. Smaller batches take `plan_num_splits`.
+    """
+    lens = [max(0, int(t)) for t in seq_lens]
+    tmax = max(lens) if lens else 0
+    flat = flat_splits_for(num_kv_heads, group, sm_count, workgroups_per_cu)
+    tiles = sum(-(-t // TILE_TOKENS) for t in lens)
+    if tiles >= MIN_FLAT_TILES_PER_WAVE * flat:
+        return 1, tmax, flat
+    splits, tmax = plan_num_splits(lens, num_kv_heads, group, sm_count)
+    return splits, tmax, 0
+
+
 class _Workspace:
     """Split-KV scratch (fp32 partial outputs and log2-sum-exps), per device.
 
@@ -123,9 +160,34 @@ class _Workspace:
                 self._buf[device] = cur
         return cur[0][:n_out].view(b, hq, splits, d), cur[1][:n_lse].view(b, hq, splits)
 
+    def get_flat(self, slots: int, hq: int, d: int, device) -> tuple[torch.Tensor, torch.Tensor]:
+        """Flat-split slots: part_out [slots, hq, d], part_lse [slots, hq]."""
+        out, lse = self.get(slots, hq, 1, d, device)
+        return out.view(slots, hq, d), lse.view(slots, hq)
+
 
 _WS = _Workspace()
 _CU_COUNT: dict[int, int] = {}
+_FLAT_WGS: dict[tuple, int] = {}
+
+
+def flat_workgroups_per_cu(kv_dtype: str, head_dim: int, scale_dtype: torch.dtype | None = None) -> int:
+    """Resident flat-kernel workgroups per CU, from the library's occupancy
+    query on the current device (a built-in table without a GPU)."""
+    sc = _abi.PA_SCALE_NONE if kv_dtype != "int8" else _SCALE_CODE.get(scale_dtype or torch.float16)
+    key = (kv_dtype, head_dim, sc)
+    n = _FLAT_WGS.get(key)
+    if n is None:
+        n = 0
+        if torch.cuda.is_available() and kv_dtype in _KV_CODE:
+            got = ctypes.c_int(0)
+            if _abi.load().pa_flat_workgroups_per_cu(_KV_CODE[kv_dtype], sc, head_dim, ctypes.byref(got)) == 0:
+                n = got.value
+        if n <= 0:
+            elem = 2 if kv_dtype in ("fp16", "bf16") else 1
+            n = _FLAT_WGS_FALLBACK.get((elem, head_dim), 2)
+        _FLAT_WGS[key] = n
+    return n
 
 
 def _cu_count(device: torch.device) -> int:
@@ -150,6 +212,7 @@ def _fill_args(
     part_out: torch.Tensor | None,
     part_lse: torch.Tensor | None,
     max_seq_len: int = 0,
+    flat_splits: int = 0,
 ) -> _abi.PaDecodeArgs:
     b, hq, d = q.shape
     shape = cache.shape
@@ -223,10 +286,16 @@ def _fill_args(
         a.scale_dtype = _SCALE_CODE[ks.dtype]
     else:
         a.scale_dtype = _abi.PA_SCALE_NONE
+    a.flat_splits = int(flat_splits)
     if part_out is not None:
         a.part_out = part_out.data_ptr()
         a.part_lse = part_lse.data_ptr()
-        a.stride_pb, a.stride_ph, a.stride_ps = part_out.stride(0), part_out.stride(1), part_out.stride(2)
+        if flat_splits > 0:  # slots [B + F, Hq, D] / [B + F, Hq]
+            if part_out.dim() != 3 or part_out.shape[0] < b + flat_splits or part_lse.shape[0] < b + flat_splits:
+                raise ValueError(f"flat split workspace needs {b + flat_splits} slots")
+            a.stride_pb, a.stride_ph, a.stride_ps = part_out.stride(0), part_out.stride(1), 0
+        else:
+            a.stride_pb, a.stride_ph, a.stride_ps = part_out.stride(0), part_out.stride(1), part_out.stride(2)
         a.stride_lb, a.stride_lh = part_lse.stride(0), part_lse.stride(1)
     return a
 
@@ -246,6 +315,7 @@ def paged_decode_hip(
     num_stages: int = 3,
     sm_scale: float | None = None,
     max_seq_len: int | None = None,
+    flat_splits: int | None = None,
 ) -> torch.Tensor:
     """Paged GQA decode attention. q: [B, Hq, D] fp16|bf16 -> [B, Hq, D] in q's dtype.
 
@@ -263,6 +333,13 @@ def paged_decode_hip(
     chunks of its own length (the reference's rule, triton_decode.py:78-85),
     except when `num_splits=None`, where the longest length is known anyway.
     Both rules compute the same attention.
+
+    `flat_splits` (an addition) selects the flat, work-balanced split: per
+    (kv head, head tile) the batch's 32-token tiles are concatenated and cut
+    into `flat_splits` equal ranges, one wave each, so ragged lengths cost no
+    tail; `num_splits` and `max_seq_len` are then unused. It needs no
+    host-side lengths, so a serving loop can pass a fixed value
+    (`flat_splits_for`).
     """
     del per_page_bt, num_warps, num_stages
     b, hq, d = q.shape
@@ -278,18 +355,26 @@ def paged_decode_hip(
         out = torch.empty((b, hq, d), dtype=q.dtype, device=q.device)
     if b == 0:
         return out
-    if num_splits is None:
+    if flat_splits:
+        num_splits = 1
+    elif num_splits is None:
         # the lengths come to the host in the one sync the reference also makes
-        num_splits, longest = plan_num_splits(cache.seq_lens.tolist(), hkv, group, _cu_count(q.device))
+        wgs = flat_workgroups_per_cu(cache.kv_dtype, d, None if cache.k_scale is None else cache.k_scale.dtype)
+        num_splits, longest, flat_splits = plan_decode(cache.seq_lens.tolist(), hkv, group,
+                                                       _cu_count(q.device), wgs)
         if max_seq_len is None:
             max_seq_len = longest
     num_splits = int(num_splits)
     scale = shape.softmax_scale if sm_scale is None else float(sm_scale)
 
     part_out = part_lse = None
-    if num_splits > 1:
+    flat = int(flat_splits or 0)
+    if flat > 0:
+        num_splits = 1
+        part_out, part_lse = _WS.get_flat(b + flat, hq, d, q.device)
+    elif num_splits > 1:
         part_out, part_lse = _WS.get(b, hq, num_splits, d, q.device)
-    args = _fill_args(q, cache, out, num_splits, scale, part_out, part_lse, max_seq_len or 0)
+    args = _fill_args(q, cache, out, num_splits, scale, part_out, part_lse, max_seq_len or 0, flat)
     lib = _abi.load()
     with torch.cuda.device(q.device):
         rc = lib.pa_decode(ctypes.byref(args), _stream(q.device))
@@ -310,21 +395,33 @@ def decode_partials(
     part_out: torch.Tensor | None = None,
     part_lse: torch.Tensor | None = None,
     max_seq_len: int = 0,
+    flat_splits: int = 0,
+    out: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Run only the decode pass; returns (part_out [B,Hq,S,D], part_lse [B,Hq,S]).
 
     part_lse is log2(sum_j 2^(s_j)) of the split's scaled logits s = q.k *
     sm_scale * log2(e) and part_out the split's normalised output, the format
     of the reference's split epilogue (triton_decode.py:169-188).
+    With `flat_splits` = F > 0 it is the flat decode pass: the partials are
+    slots [B + F, Hq, D] / [B + F, Hq], and sequences that one wave range
+    holds whole are written to `out`.
     """
     b, hq, d = q.shape
     scale = cache.shape.softmax_scale if sm_scale is None else float(sm_scale)
+    if flat_splits > 0:
+        num_splits = 1
+        if part_out is None:
+            part_out = torch.empty((b + flat_splits, hq, d), dtype=torch.float32, device=q.device)
+        if part_lse is None:
+            part_lse = torch.empty((b + flat_splits, hq), dtype=torch.float32, device=q.device)
     if part_out is None:
         part_out = torch.empty((b, hq, num_splits, d), dtype=torch.float32, device=q.device)
     if part_lse is None:
         part_lse = torch.empty((b, hq, num_splits), dtype=torch.float32, device=q.device)
-    out = torch.empty((b, hq, d), dtype=q.dtype, device=q.device)
-    args = _fill_args(q, cache, out, num_splits, scale, part_out, part_lse, max_seq_len)
+    if out is None:
+        out = torch.empty((b, hq, d), dtype=q.dtype, device=q.device)
+    args = _fill_args(q, cache, out, num_splits, scale, part_out, part_lse, max_seq_len, flat_splits)
     lib = _abi.load()
     with torch.cuda.device(q.device):
         rc = lib.pa_decode_partials(ctypes.byref(args), _stream(q.device))
@@ -362,7 +459,7 @@ def split_reduce(
 
 
 def split_count_for(cache: PagedKVCache, device: torch.device) -> int:
-    """The split count `paged_decode_hip(num_splits=None)` would choose."""
+    """The classic split count `plan_num_splits` gives this batch."""
     return plan_num_splits(cache.seq_lens.tolist(), cache.shape.num_kv_heads, cache.shape.gqa_group,
                            _cu_count(device))[0]
 
@@ -375,6 +472,9 @@ __all__ = [
     "split_reduce",
     "split_count_for",
     "plan_num_splits",
+    "plan_decode",
+    "flat_splits_for",
+    "flat_workgroups_per_cu",
     "WAVES_PER_WORKGROUP",
     "TILE_TOKENS",
 ]

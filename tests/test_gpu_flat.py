@@ -1,0 +1,158 @@
+"""GPU parity of the flat (work-balanced) split against the CPU oracle.
+
+The flat split has no counterpart in the reference; its result is the same
+attention (pagedattn/reference.py:28-49), so every case is held to the
+decode's bar: max |HIP - oracle_fp32| < 2e-3, and the partial slots of the
+decode pass to the oracle's restatement of the same ranges
+(oracle.flat_partials). Cases cover ranges that cut sequences, sequences
+inside one range, empty and 1-token sequences, more ranges than tiles, one
+range for the whole batch, GQA groups above 16, every KV dtype and page
+sizes above 16.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from helpers import max_abs, seeded_q
+from oracle import reference as oracle
+from pagedattn import LLAMA3_8B, LLAMA3_70B, QWEN25_05B, ModelShape, allocate
+from pagedattn.hip_decode import decode_partials, paged_decode_hip
+
+pytestmark = pytest.mark.gpu
+
+ABS_TOL = 2e-3
+
+RAGGED = [300, 1, 4096, 0, 17, 33, 64, 1000]
+
+
+def _case(shape, lens, kv_dtype="fp16", block_size=16, seed=0, scale_dtype=torch.float16):
+    c = allocate(shape, len(lens), lens, block_size=block_size, kv_dtype=kv_dtype, seed=seed,
+                 scale_dtype=scale_dtype, device="cuda")
+    q = seeded_q(len(lens), shape.num_q_heads, shape.head_dim, seed, device="cuda")
+    return q, c
+
+
+def _check(q, c, flat, tol=ABS_TOL):
+    # the reference's BLOCK_N rule: a multiple of the page size
+    got = paged_decode_hip(q, c, flat_splits=flat, block_n=max(64, c.block_size))
+    torch.cuda.synchronize()
+    want = oracle.reference_decode(q, c, out_dtype=torch.float32)
+    lens = c.seq_lens.cpu().tolist()
+    live = [b for b, t in enumerate(lens) if t > 0]
+    dead = [b for b, t in enumerate(lens) if t == 0]
+    err = max_abs(got[live], want[live]) if live else 0.0
+    print(f"flat={flat} lens={lens[:8]} max_abs={err:.2e}")
+    assert err < tol
+    if dead:
+        assert torch.equal(got[dead].float().cpu(), torch.zeros_like(want[dead]))
+    return got
+
+
+@pytest.mark.parametrize("flat", [1, 2, 3, 7, 64, 1000])
+def test_flat_ragged_fp16(flat):
+    q, c = _case(LLAMA3_8B, RAGGED, seed=1)
+    _check(q, c, flat)
+
+
+@pytest.mark.parametrize("kv_dtype,scale_dtype", [("fp8_e5m2", torch.float16), ("int8", torch.float16),
+                                                  ("int8", torch.float32), ("bf16", torch.float16)])
+@pytest.mark.parametrize("flat", [5, 96])
+def test_flat_kv_dtypes(kv_dtype, scale_dtype, flat):
+    q, c = _case(LLAMA3_8B, RAGGED, kv_dtype=kv_dtype, seed=2, scale_dtype=scale_dtype)
+    _check(q, c, flat)
+
+
+@pytest.mark.parametrize("shape,lens,flat", [
+    (QWEN25_05B, [32, 192, 77, 5, 0, 160], 9),              # group 7, head_dim 64
+    (LLAMA3_70B, [513, 2, 1500], 11),                        # group 8
+    (ModelShape(40, 2, 128, "g20"), [700, 31, 2049], 6),     # group 20: two head tiles
+    (ModelShape(8, 8, 32, "d32"), [129, 64, 3], 4),          # head_dim 32
+    (ModelShape(8, 4, 256, "d256"), [300, 1, 95], 5),        # head_dim 256
+    (ModelShape(8, 8, 64, "mha"), [1, 1, 1, 1], 3),          # 1-token sequences
+])
+def test_flat_shapes(shape, lens, flat):
+    q, c = _case(shape, lens, seed=3)
+    _check(q, c, flat)
+
+
+@pytest.mark.parametrize("block_size", [32, 64, 256])
+def test_flat_page_sizes(block_size):
+    q, c = _case(LLAMA3_8B, [700, 5, 1900, 33], block_size=block_size, seed=4)
+    _check(q, c, 13)
+
+
+def test_flat_all_empty():
+    q, c = _case(LLAMA3_8B, [0, 0, 0], seed=5)
+    got = paged_decode_hip(q, c, flat_splits=8)
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu(), torch.zeros_like(got.cpu()))
+
+
+def test_flat_bf16_io():
+    q, c = _case(LLAMA3_8B, RAGGED, kv_dtype="bf16", seed=6)
+    qb = q.to(torch.bfloat16)
+    got = paged_decode_hip(qb, c, flat_splits=21)
+    torch.cuda.synchronize()
+    assert got.dtype == torch.bfloat16
+    want = oracle.reference_decode(qb, c, out_dtype=torch.float32)
+    live = [b for b, t in enumerate(RAGGED) if t > 0]
+    err = (got[live].float().cpu() - want[live]).abs()
+    assert bool((err <= ABS_TOL + 2.0 ** -8 * want[live].abs()).all())
+
+
+def test_flat_bit_stable_and_matches_classic_split():
+    q, c = _case(LLAMA3_8B, RAGGED, seed=7)
+    a = paged_decode_hip(q, c, flat_splits=37).clone()
+    b = paged_decode_hip(q, c, flat_splits=37)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    classic = paged_decode_hip(q, c, num_splits=6, max_seq_len=max(RAGGED))
+    torch.cuda.synchronize()
+    assert max_abs(a.float(), classic.float().cpu()) < ABS_TOL
+
+
+@pytest.mark.parametrize("flat", [3, 16])
+def test_flat_partial_slots_match_oracle(flat):
+    """The decode pass alone: every slot a range writes equals the oracle's
+    partial of the same token range, and sequences held by one range are
+    already final in `out`."""
+    lens = [300, 1, 900, 0, 64, 33]
+    q, c = _case(LLAMA3_8B, lens, seed=8)
+    b, hq, d = q.shape
+    part = torch.full((b + flat, hq, d), float("nan"), device="cuda")
+    lse = torch.full((b + flat, hq), float("nan"), device="cuda")
+    out = torch.zeros_like(q)
+    decode_partials(q, c, 1, part_out=part, part_lse=lse, flat_splits=flat, out=out)
+    torch.cuda.synchronize()
+    opart, olse, whole = oracle.flat_partials(q, c, flat)
+    segs, _ = oracle.flat_segments(lens, flat)
+    ref = oracle.reference_decode(q, c, out_dtype=torch.float32)
+    written = set()
+    for j, bb, _, _ in segs:
+        if whole[bb]:
+            continue
+        written.add(bb + j)
+    for slot in sorted(written):
+        # P enters the PV product in fp16, as in the decode: the decode's bar
+        assert max_abs(part[slot], opart[slot]) < ABS_TOL
+        assert (lse[slot].cpu() - olse[slot]).abs().max().item() < 1e-3
+    for bb, w in enumerate(whole):
+        if w:
+            assert max_abs(out[bb], ref[bb]) < ABS_TOL
+
+
+@pytest.mark.parametrize("kv_dtype,scale_dtype", [("fp16", None), ("bf16", None), ("fp8_e5m2", None),
+                                                  ("int8", torch.float16), ("int8", torch.float32)])
+@pytest.mark.parametrize("d", [32, 64, 128, 256])
+def test_flat_occupancy_query(kv_dtype, scale_dtype, d):
+    """The library's occupancy answer sizes flat_splits; at head_dim 128 (the
+    BASELINE shapes) it must equal the no-GPU fallback table."""
+    from pagedattn.hip_decode import _FLAT_WGS_FALLBACK, flat_workgroups_per_cu
+
+    n = flat_workgroups_per_cu(kv_dtype, d, scale_dtype)
+    print(f"{kv_dtype} d={d}: {n} workgroups/CU")
+    assert 1 <= n <= 8
+    if d == 128:
+        assert n == _FLAT_WGS_FALLBACK[(2 if kv_dtype in ("fp16", "bf16") else 1, d)]

@@ -83,7 +83,7 @@ def test_constants_match_header():
     for name in ("PA_ABI_VERSION", "PA_OK", "PA_ERR_INVALID", "PA_ERR_UNSUPPORTED", "PA_ERR_HIP",
                  "PA_KV_FP16", "PA_KV_FP8_E5M2", "PA_KV_INT8", "PA_SCALE_NONE", "PA_SCALE_FP16",
                  "PA_SCALE_FP32", "PA_IO_FP16", "PA_MAX_SPLITS", "PA_MAX_GROUP", "PA_KV_BF16",
-                 "PA_IO_BF16"):
+                 "PA_IO_BF16", "PA_MAX_FLAT_SPLITS"):
         m = re.search(rf"#define {name} \(?(-?\d+)\)?", text)
         assert m, name
         assert int(m.group(1)) == getattr(_abi, name), name
@@ -139,6 +139,11 @@ INVALID = [
     ("no_blocks", dict(num_blocks=0), _abi.PA_ERR_INVALID),
     ("misaligned_workspace", dict(num_splits=2, part_out=FAKE + 4, part_lse=FAKE,
                                   stride_pb=1, stride_ph=1, stride_ps=128), _abi.PA_ERR_INVALID),
+    ("flat_negative", dict(flat_splits=-1), _abi.PA_ERR_INVALID),
+    ("flat_big", dict(flat_splits=_abi.PA_MAX_FLAT_SPLITS + 1), _abi.PA_ERR_INVALID),
+    ("flat_no_workspace", dict(flat_splits=4), _abi.PA_ERR_INVALID),
+    ("flat_misaligned_workspace", dict(flat_splits=4, part_out=FAKE + 4, part_lse=FAKE,
+                                       stride_pb=32 * 128, stride_ph=128), _abi.PA_ERR_INVALID),
 ]
 
 
@@ -325,3 +330,41 @@ def test_plan_num_splits():
     assert plan_num_splits([], 8, 4, 256) == (1, 0)
     assert plan_num_splits([0, 0], 8, 4, 256) == (1, 0)
     assert plan_num_splits([1], 1, 1, 256)[0] == 1
+
+
+def test_flat_splits_for_and_plan_decode():
+    from pagedattn import flat_splits_for, plan_decode
+
+    # one round of resident waves over the (kv head, head tile) units
+    assert flat_splits_for(8, 4, 256, 3) == 384
+    assert flat_splits_for(8, 4, 256, 2) == 256
+    assert flat_splits_for(2, 20, 256, 2) == 512      # group 20: two head tiles
+    assert flat_splits_for(64, 1, 4, 1) == 1
+    # every BASELINE split shape takes the flat split ...
+    assert plan_decode([4096] * 64, 8, 4, 256, 2) == (1, 4096, 256)
+    assert plan_decode([16384] * 32, 8, 8, 256, 3) == (1, 16384, 384)
+    assert plan_decode([131072] * 4, 8, 4, 256, 2) == (1, 131072, 256)
+    # ... and a latency-bound batch (too few tiles per wave) the classic path
+    s, m, f = plan_decode([192] * 24, 2, 7, 256, 4)
+    assert f == 0 and s >= 1 and m == 192
+    assert plan_decode([], 8, 4, 256) == (1, 0, 0)
+    # the threshold: MIN_FLAT_TILES_PER_WAVE tiles per wave
+    from pagedattn.hip_decode import MIN_FLAT_TILES_PER_WAVE
+    f = flat_splits_for(1, 1, 1, 1)
+    assert f == 4
+    assert plan_decode([32 * MIN_FLAT_TILES_PER_WAVE * f], 1, 1, 1, 1)[2] == f
+    assert plan_decode([32 * MIN_FLAT_TILES_PER_WAVE * f - 32], 1, 1, 1, 1)[2] == 0
+
+
+@cpu_only
+def test_flat_occupancy_query_validates_before_hip():
+    lib = _lib()
+    out = ctypes.c_int(7)
+    assert lib.pa_flat_workgroups_per_cu(_abi.PA_KV_FP16, _abi.PA_SCALE_NONE, 96, ctypes.byref(out)) \
+        == _abi.PA_ERR_UNSUPPORTED
+    assert out.value == 0
+    assert lib.pa_flat_workgroups_per_cu(_abi.PA_KV_INT8, _abi.PA_SCALE_NONE, 128, ctypes.byref(out)) \
+        == _abi.PA_ERR_INVALID
+    assert lib.pa_flat_workgroups_per_cu(_abi.PA_KV_FP16, _abi.PA_SCALE_NONE, 128, None) \
+        == _abi.PA_ERR_INVALID
+    assert lib.pa_last_error().decode()

@@ -286,6 +286,61 @@ def test_split_ranges_closed_form():
     assert oracle.split_ranges(4096, 8, 64) == [(512 * i, 512 * i + 512) for i in range(8)]
 
 
+def test_flat_segments_known_answer():
+    # tiles [4, 0, 2] (align 32), total 6, per = ceil(6 / 2) = 3
+    segs, per = oracle.flat_segments([100, 0, 33], 2)
+    assert per == 3
+    assert segs == [(0, 0, 0, 96), (1, 0, 96, 100), (1, 2, 0, 33)]
+    # one range holds everything; more ranges than tiles leave ranges idle
+    assert oracle.flat_segments([100, 0, 33], 1)[0] == [(0, 0, 0, 100), (0, 2, 0, 33)]
+    segs, per = oracle.flat_segments([64, 1], 50)
+    assert per == 1 and segs == [(0, 0, 0, 32), (1, 0, 32, 64), (2, 1, 0, 1)]
+    assert oracle.flat_segments([0, 0], 4) == ([], 1)
+
+
+@pytest.mark.parametrize("flat_splits", [1, 2, 5, 13, 64, 500])
+def test_flat_segments_partition(flat_splits):
+    g = torch.Generator().manual_seed(21)
+    lens = torch.randint(0, 3000, (37,), generator=g).tolist()
+    lens[3] = 0
+    lens[10] = 1
+    segs, per = oracle.flat_segments(lens, flat_splits)
+    # every sequence is covered exactly once, in order, by tile-aligned pieces
+    for b, t in enumerate(lens):
+        mine = [(lo, hi) for _, bb, lo, hi in segs if bb == b]
+        pos = 0
+        for lo, hi in mine:
+            assert lo == pos and lo % 32 == 0 and hi > lo
+            pos = hi
+        assert pos == t
+    # a range holds at most `per` tiles, ranges are in order, slots are unique
+    tiles = {}
+    for j, _, lo, hi in segs:
+        tiles[j] = tiles.get(j, 0) + -(-(hi - lo) // 32)
+    assert max(tiles.values()) <= per and max(tiles) < flat_splits
+    assert [j for j, *_ in segs] == sorted(j for j, *_ in segs)
+    slots = [b + j for j, b, _, _ in segs]
+    assert len(set(slots)) == len(slots)
+
+
+@pytest.mark.parametrize("flat_splits", [1, 3, 8, 40])
+def test_flat_partials_merge_to_reference(flat_splits):
+    lens = [1, 33, 500, 0, 96, 260]
+    c = _cache(LLAMA3_8B, lens, seed=15)
+    q = _q(6, 32, 128, 15)
+    part, lse, whole = oracle.flat_partials(q, c, flat_splits)
+    ref = c_oracle.decode(q, c)
+    segs, _ = oracle.flat_segments(lens, flat_splits)
+    for b, t in enumerate(lens):
+        js = [j for j, bb, _, _ in segs if bb == b]
+        assert whole[b] == (len(js) == 1)
+        if not js:
+            continue
+        merged = oracle.split_merge(part[[b + j for j in js]].permute(1, 0, 2).unsqueeze(0),
+                                    lse[[b + j for j in js]].T.unsqueeze(0))[0]
+        assert (merged.double() - ref[b]).abs().max().item() < 2e-5
+
+
 def test_merge_of_all_empty_splits_is_nan():
     part = torch.zeros((1, 1, 3, 4))
     lse = torch.full((1, 1, 3), float("-inf"))
