@@ -364,25 +364,55 @@ def main() -> int:
     kern_us = ev0.elapsed_time(ev1) / args.steps * 1e3
     _log(f"decode kernel alone: {kern_us:.1f} us/launch")
 
+    # The merge pass alone. It is a few microseconds of GPU work, less than
+    # one Python launch, so back-to-back eager launches would time the host:
+    # the launches are captured in a HIP graph and the graph is replayed.
     reduce_us = None
-    if splits > 1:
+    merge = None
+    if flat:
+        from pagedattn.hip_decode import flat_merge
+
+        run(caches[0])  # the slots of one pass
+        merge = lambda: flat_merge(q, caches[0], flat, fo, fl, out)
+    elif splits > 1:
         from pagedattn.hip_decode import split_reduce
 
-        for _ in range(args.warmup):
-            split_reduce(part_out, part_lse, out)
+        merge = lambda: split_reduce(part_out, part_lse, out)
+    if merge is not None:
+        merge()
+        torch.cuda.synchronize()
+        eager = out.clone()
+        inner, outer = 20, max(1, args.steps // 20)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            merge()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(inner):
+                merge()
+        graph.replay()
+        torch.cuda.synchronize()
         ev0.record()
-        for _ in range(args.steps):
-            split_reduce(part_out, part_lse, out)
+        for _ in range(outer):
+            graph.replay()
         ev1.record()
         torch.cuda.synchronize()
-        reduce_us = ev0.elapsed_time(ev1) / args.steps * 1e3
-        _log(f"split reduce alone: {reduce_us:.2f} us/launch")
+        reduce_us = ev0.elapsed_time(ev1) / (inner * outer) * 1e3
+        if not torch.equal(out, eager):
+            _log("MERGE GRAPH REPLAY DIFFERS FROM THE EAGER MERGE")
+            return 1
+        _log(f"merge pass alone: {reduce_us:.2f} us/launch (graph of {inner} launches x {outer})")
 
+    kernel_name = "paged_decode_flat_kernel" if flat else "paged_decode_kernel"
     traffic = None
     tfile = ROOT / "profiles" / "traffic.json"
     if tfile.exists():
         try:
-            traffic = json.loads(tfile.read_text()).get(wl.name, {}).get("hbm_bytes_per_launch")
+            entry = json.loads(tfile.read_text()).get(wl.name, {})
+            if entry.get("kernel") == kernel_name:
+                traffic = entry.get("hbm_bytes_per_launch")
         except (OSError, ValueError):
             traffic = None
 
@@ -428,7 +458,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved_kernel / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "paged_decode_kernel",
+            "kernel": kernel_name,
             "kernel_us": round(kern_us, 2),
         },
         "cpu_baseline": None,

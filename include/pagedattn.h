@@ -214,6 +214,14 @@ typedef struct pa_cache_write_args {
  * caches in this library's formats. */
 int pa_cache_write(const pa_cache_write_args *args, void *stream);
 
+/* The flat split's merge pass alone (flat_splits > 0): folds the partial
+ * slots that pa_decode_partials with the same arguments wrote into `out`
+ * (sequences that one range held whole are already there; empty sequences
+ * get zeros). pa_decode_partials + pa_flat_merge == pa_decode. The
+ * counterpart of the reference's `_split_reduce_kernel` launch
+ * (pagedattn/triton_decode.py:368-376) for the flat split. */
+int pa_flat_merge(const pa_decode_args *args, void *stream);
+
 /* Workgroups of the flat decode kernel for (kv_dtype, scale_dtype,
  * head_dim) that one CU holds at once (hipOccupancyMaxActiveBlocksPerMultiprocessor
  * on the current device), written to *out. A host planner sizes

@@ -39,9 +39,15 @@
 //
 // Quantised KV is dequantised in registers with one v_perm per fp16 pair:
 //   fp8_e5m2 -> fp16: the e5m2 byte is the high byte of the fp16 pattern.
-//   int8 -> fp16 exactly (|x| <= 127): 0x64 | (b ^ 0x80) is 1152 + x as fp16,
-//           and 1152 is subtracted in fp16; the per-(token, head) scale is
-//           folded into the fp32 score (K) and into the probability (V).
+//   int8 -> fp16 exactly (|x| <= 127): with the byte's sign bit flipped
+//           (one xor per 4 K bytes, per 2 V bytes), b ^ 0x80 = x + 128 is the
+//           mantissa of an fp16 denormal, (x + 128) * 2^-24 (the MFMA keeps
+//           fp16 denormals). The offset is removed after the products, once
+//           per row instead of per element: from each score as
+//           2^-17 * sum(q) of its head, from the output as 2^-17 * sum(P)
+//           of its column (P summed in fp32 by v_dot2); 2^24 is folded into
+//           the scales. The per-(token, head) scale is folded into the
+//           fp32 score (K) and into the probability (V).
 
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
@@ -66,7 +72,9 @@ constexpr int kWaves = 4;          // waves per workgroup
 constexpr int kSplitAlign = 32;    // split ranges are multiples of this many tokens
 constexpr float kRescaleLog2 = 8.0f;
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr uint32_t kInt8Xor = 0x64806480u;  // [b, 0, b', 0] -> [b ^ 0x80, 0x64, b' ^ 0x80, 0x64]
+constexpr uint32_t kInt8Sign = 0x80808080u;      // int8 x -> x + 128 in every byte
+constexpr uint32_t kInt8PairSign = 0x00800080u;  // the same for [b, 0, b', 0]
+constexpr float kInt8Unit = 16777216.0f;      // 2^24: int8 operands are (x + 128) * 2^-24
 
 struct KParams {
   const uint8_t *q;
@@ -170,21 +178,9 @@ __device__ __forceinline__ void store_row(uint8_t *dst, const float *y, int n, b
   }
 }
 
-// int8 operands hold 1152 + x; remove the offset (exact in fp16).
-template <int KV>
-__device__ __forceinline__ f16x8 finish(f16x8 x) {
-  if constexpr (KV == PA_KV_INT8) {
-    const _Float16 off = (_Float16)1152.0f;
-    const f16x8 o = {off, off, off, off, off, off, off, off};
-    return x - o;
-  } else {
-    return x;
-  }
-}
-
 // Selector placing byte i of `lo` and byte j of `hi` into the two halves of a
-// dword: as the high byte (fp8 e5m2 -> fp16) or the low byte (int8, before the
-// kInt8Xor that turns [b, 0] into 0x64 | b ^ 0x80).
+// dword: as the high byte (fp8 e5m2 -> fp16) or the low byte (int8 with its
+// sign bit flipped -> the fp16 denormal (x + 128) * 2^-24).
 template <int KV>
 __device__ __forceinline__ constexpr uint32_t pair_sel(uint32_t i, uint32_t j) {
   if constexpr (KV == PA_KV_INT8) {
@@ -194,12 +190,11 @@ __device__ __forceinline__ constexpr uint32_t pair_sel(uint32_t i, uint32_t j) {
   }
 }
 
-// Two stored bytes -> two fp16 bit patterns (one v_perm, plus a xor for int8).
+// Two stored bytes -> two fp16 bit patterns: one v_perm (int8 words arrive
+// with the sign bits already flipped).
 template <int KV>
 __device__ __forceinline__ uint32_t bytes_to_halves(uint32_t hi, uint32_t lo, uint32_t sel) {
-  const uint32_t w = perm(hi, lo, sel);
-  if constexpr (KV == PA_KV_INT8) return w ^ kInt8Xor;
-  return w;
+  return perm(hi, lo, sel);
 }
 
 // One K/V load. K and V are streamed exactly once per call, so they are
@@ -291,7 +286,26 @@ struct WaveState {
   f32x4 acc[G::kE];       // O^T accumulators, one 16x16 block per d-slab
   float m;                // running max (log2 domain) for head column r16
   float l;                // running sum over this lane's tokens
+  // int8 only: 2^-17 * sum(q) of head r16 (the offset in every raw score)
+  // and the sum of this lane's P values (2^-17 times their column sum is
+  // the offset in every output row)
+  float qcorr;
+  float wsum;
 };
+
+// int8: take the offsets out of the accumulators,
+// O = (acc - 2^-17 * sum(P)) * 2^24.
+template <int KV, int D>
+__device__ __forceinline__ void remove_offsets(WaveState<KV, D> &st) {
+  using G = Geo<KV, D>;
+  if constexpr (KV == PA_KV_INT8) {
+    const float off = col_sum(st.wsum) * (1.0f / 131072.0f);
+#pragma unroll
+    for (int sl = 0; sl < G::kE; ++sl)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) st.acc[sl][i] = (st.acc[sl][i] - off) * kInt8Unit;
+  }
+}
 
 // Issue the loads of the tile starting at token n0 (< hi). Rows at or past
 // `hi` in the last tile are clamped to valid rows of the sequence: they are
@@ -389,29 +403,24 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  // ---- int8 scales of this lane's tokens {16u + 4c + i} via LDS (the V
-  // scales are read back only for the P operand, to keep them out of the
-  // registers live across the QK products) ----
-  float ksc[NV];
+  // ---- int8 scales of this tile into the wave's LDS slot; each lane reads
+  // back those of its tokens {16u + 4c + i} where they are used (K after the
+  // QK products, V for the P operand), so none are live across the MFMAs ----
   if constexpr (KV == PA_KV_INT8) {
 #pragma unroll
     for (int j = 0; j < G::kScales / 64; ++j) sc_lds[j * 64 + lane] = r.sc[j];
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-    for (int u = 0; u < NS; ++u) {
-      const f32x4 kq = *reinterpret_cast<const f32x4 *>(sc_lds + 16 * u + 4 * c);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) ksc[4 * u + i] = kq[i];
-    }
   }
 
-  // ---- S^T = K Q^T, one 16-token sub-tile at a time ----
+  // ---- S^T = K Q^T, one 16-token sub-tile at a time (int8: the
+  // accumulator starts at -2^-17 * sum(q), the operands' offset) ----
   f32x4 sacc[NS];
 #pragma unroll
   for (int u = 0; u < NS; ++u) {
     f32x4 a = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (KV == PA_KV_INT8) a = f32x4{-st.qcorr, -st.qcorr, -st.qcorr, -st.qcorr};
 #pragma unroll
     for (int ks = 0; ks < G::kKSteps; ++ks) {
       f16x8 kop;
@@ -422,12 +431,16 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
         kop = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4 *>(src));
       } else {
         const u32x2 w = *reinterpret_cast<const u32x2 *>(src);
-        const uint32_t w0 = w.x;
-        const uint32_t w1 = w.y;
-        kop = finish<KV>(as_f16x8(bytes_to_halves<KV>(w0, w0, pair_sel<KV>(0, 1)),
-                                  bytes_to_halves<KV>(w0, w0, pair_sel<KV>(2, 3)),
-                                  bytes_to_halves<KV>(w1, w1, pair_sel<KV>(0, 1)),
-                                  bytes_to_halves<KV>(w1, w1, pair_sel<KV>(2, 3))));
+        uint32_t w0 = w.x;
+        uint32_t w1 = w.y;
+        if constexpr (KV == PA_KV_INT8) {
+          w0 ^= kInt8Sign;
+          w1 ^= kInt8Sign;
+        }
+        kop = as_f16x8(bytes_to_halves<KV>(w0, w0, pair_sel<KV>(0, 1)),
+                       bytes_to_halves<KV>(w0, w0, pair_sel<KV>(2, 3)),
+                       bytes_to_halves<KV>(w1, w1, pair_sel<KV>(0, 1)),
+                       bytes_to_halves<KV>(w1, w1, pair_sel<KV>(2, 3)));
       }
       a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, st.qop[ks], a, 0, 0, 0);
     }
@@ -439,11 +452,17 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
 
   // ---- online softmax over the tokens this lane holds for head r16 ----
   float s[NV];
+  if constexpr (KV == PA_KV_INT8) {
+    const float unit_scale = p.qk_scale * kInt8Unit;
 #pragma unroll
-  for (int e = 0; e < NV; ++e) {
-    float x = sacc[e >> 2][e & 3] * p.qk_scale;
-    if constexpr (KV == PA_KV_INT8) x *= ksc[e];
-    s[e] = x;
+    for (int u = 0; u < NS; ++u) {
+      const f32x4 kq = *reinterpret_cast<const f32x4 *>(sc_lds + 16 * u + 4 * c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[4 * u + i] = sacc[u][i] * (kq[i] * unit_scale);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < NV; ++e) s[e] = sacc[e >> 2][e & 3] * p.qk_scale;
   }
   if (tail) {
 #pragma unroll
@@ -464,6 +483,7 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
     st.l *= alpha;
 #pragma unroll
     for (int sl = 0; sl < G::kE; ++sl) st.acc[sl] *= alpha;
+    if constexpr (KV == PA_KV_INT8) st.wsum *= alpha;
     st.m = m_new;
   }
 
@@ -491,26 +511,47 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
 #pragma unroll
       for (int e = 0; e < 8; ++e) pop[e] = (_Float16)pr[8 * pp + e];
     }
+    if constexpr (G::kElem == 2) {
 #pragma unroll
-    for (int sl = 0; sl < G::kE; ++sl) {
-      uint32_t h[4];
+      for (int sl = 0; sl < G::kE; ++sl) {
+        uint32_t h[4];
 #pragma unroll
-      for (int m2 = 0; m2 < 4; ++m2) {
-        const uint32_t *lo = r.v[8 * pp + 2 * m2];
-        const uint32_t *hi2 = r.v[8 * pp + 2 * m2 + 1];
-        if constexpr (G::kElem == 2) {
+        for (int m2 = 0; m2 < 4; ++m2) {
           const int wi = sl >> 1;
           const uint32_t sel = (sl & 1) ? 0x07060302u : 0x05040100u;
-          h[m2] = perm(hi2[wi], lo[wi], sel);
+          h[m2] = perm(r.v[8 * pp + 2 * m2 + 1][wi], r.v[8 * pp + 2 * m2][wi], sel);
           if constexpr (KV == PA_KV_BF16) h[m2] = bf16x2_to_f16x2(h[m2]);
-        } else {
-          const int wi = sl >> 2;
-          const uint32_t b = sl & 3;
-          h[m2] = bytes_to_halves<KV>(hi2[wi], lo[wi], pair_sel<KV>(b, b));
         }
+        const f16x8 vop = as_f16x8(h[0], h[1], h[2], h[3]);
+        st.acc[sl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop, st.acc[sl], 0, 0, 0);
       }
-      const f16x8 vop = finish<KV>(as_f16x8(h[0], h[1], h[2], h[3]));
-      st.acc[sl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop, st.acc[sl], 0, 0, 0);
+    } else {
+      // word wi of a row holds head-dim elements 4*wi .. 4*wi+3 of the lane's
+      // slab group (int8: the pair's sign bits are flipped after the perm,
+      // which keeps the tile registers as loaded)
+#pragma unroll
+      for (int sl = 0; sl < G::kE; ++sl) {
+        const int wi = sl >> 2;
+        const uint32_t b = sl & 3;
+        uint32_t h[4];
+#pragma unroll
+        for (int m2 = 0; m2 < 4; ++m2) {
+          h[m2] = bytes_to_halves<KV>(r.v[8 * pp + 2 * m2 + 1][wi], r.v[8 * pp + 2 * m2][wi],
+                                      pair_sel<KV>(b, b));
+          if constexpr (KV == PA_KV_INT8) h[m2] ^= kInt8PairSign;
+        }
+        const f16x8 vop = as_f16x8(h[0], h[1], h[2], h[3]);
+        st.acc[sl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop, st.acc[sl], 0, 0, 0);
+      }
+    }
+    if constexpr (KV == PA_KV_INT8) {
+      // sum(P) of this lane's tokens, exactly the P the MFMAs saw
+      const f16x2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const f16x2 pp2 = {pop[e], pop[e + 1]};
+        st.wsum = __builtin_amdgcn_fdot2(pp2, one2, st.wsum, false);
+      }
     }
   }
   if constexpr (KV == PA_KV_INT8) {
@@ -538,6 +579,15 @@ __device__ __forceinline__ void load_q(WaveState<KV, D> &st, const KParams &p, i
     }
     st.qop[ks] = qv;
   }
+  if constexpr (KV == PA_KV_INT8) {
+    // 2^-17 * sum over head_dim of this head's q (lane c holds 8 of every 32)
+    float qs = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < G::kKSteps; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qs += (float)st.qop[ks][e];
+    st.qcorr = col_sum(qs) * (1.0f / 131072.0f);
+  }
 }
 
 template <int KV, int D>
@@ -547,6 +597,7 @@ __device__ __forceinline__ void reset_state(WaveState<KV, D> &st) {
   st.l = 0.f;
 #pragma unroll
   for (int sl = 0; sl < G::kE; ++sl) st.acc[sl] = f32x4{0.f, 0.f, 0.f, 0.f};
+  st.wsum = 0.f;
 }
 
 // One lane's share of a finished row of head h: y[0 .. 4*kE) = O[h][d0 ..)
@@ -783,6 +834,8 @@ paged_decode_kernel(const KParams p) {
     }
   }
 
+  remove_offsets(st);
+
   // ---- merge the waves through LDS ----
   const float lw = col_sum(st.l);
   if (c == 0) {
@@ -979,6 +1032,7 @@ paged_decode_flat_kernel(const KParams p) {
   auto post = [&](int i) {
     const bool seq_end = cc.t + 1 == cc.tiles;
     if (seq_end || i + 1 == n) {
+      remove_offsets(st);
       const float L = col_sum(st.l);
       const float inv = (L > 0.f) ? 1.0f / L : 0.f;
       if (r16 < nh) {
@@ -1520,6 +1574,25 @@ int pa_decode_partials(const pa_decode_args *a, void *stream) {
   hipError_t e = launch_decode(k, a, a->flat_splits > 0 ? kFlat : kPartials,
                                static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(PA_ERR_HIP, "decode launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int pa_flat_merge(const pa_decode_args *a, void *stream) {
+  KParams k;
+  int rc = build_params(a, true, &k);
+  if (rc != PA_OK) return rc;
+  if (a->flat_splits <= 0) return fail(PA_ERR_INVALID, "pa_flat_merge needs flat_splits > 0");
+  pa_reduce_args ra = reduce_args_from(a);
+  ra.num_splits = 1;
+  RParams rp;
+  rc = check_reduce(&ra, &rp);
+  if (rc != PA_OK) return rc;
+  rp.seq_lens = a->seq_lens;
+  rp.max_tokens = k.max_tokens;
+  rp.num_splits = a->flat_splits;
+  if (a->batch == 0) return ok();
+  hipError_t e = launch_reduce<kMergeFlat>(rp, a->batch, a->head_dim, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(PA_ERR_HIP, "reduce launch failed: %s", hipGetErrorString(e));
   return ok();
 }
 

@@ -43,6 +43,7 @@ EXPORTED_SYMBOLS = (
     "pa_decode_partials",
     "pa_split_reduce",
     "pa_cache_write",
+    "pa_flat_merge",
     "pa_flat_workgroups_per_cu",
     "pa_last_error",
     "pa_abi_version",
@@ -183,6 +184,8 @@ def load() -> ctypes.CDLL:
         lib.pa_split_reduce.restype = ctypes.c_int
         lib.pa_cache_write.argtypes = [ctypes.POINTER(PaCacheWriteArgs), _vp]
         lib.pa_cache_write.restype = ctypes.c_int
+        lib.pa_flat_merge.argtypes = [ctypes.POINTER(PaDecodeArgs), _vp]
+        lib.pa_flat_merge.restype = ctypes.c_int
         lib.pa_flat_workgroups_per_cu.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                                   ctypes.POINTER(ctypes.c_int)]
         lib.pa_flat_workgroups_per_cu.restype = ctypes.c_int

@@ -429,6 +429,29 @@ def decode_partials(
     return part_out, part_lse
 
 
+def flat_merge(
+    q: torch.Tensor,
+    cache: PagedKVCache,
+    flat_splits: int,
+    part_out: torch.Tensor,
+    part_lse: torch.Tensor,
+    out: torch.Tensor,
+    sm_scale: float | None = None,
+) -> torch.Tensor:
+    """The flat split's merge pass alone: after `decode_partials(...,
+    flat_splits=F, out=out)` with the same arguments, folds the slots into
+    `out` (the pair equals `paged_decode_hip(..., flat_splits=F)`)."""
+    if flat_splits <= 0:
+        raise ValueError("flat_merge needs flat_splits > 0")
+    scale = cache.shape.softmax_scale if sm_scale is None else float(sm_scale)
+    args = _fill_args(q, cache, out, 1, scale, part_out, part_lse, 0, flat_splits)
+    lib = _abi.load()
+    with torch.cuda.device(q.device):
+        rc = lib.pa_flat_merge(ctypes.byref(args), _stream(q.device))
+    _abi.check(rc, "pa_flat_merge")
+    return out
+
+
 def split_reduce(
     part_out: torch.Tensor, part_lse: torch.Tensor, out: torch.Tensor | None = None
 ) -> torch.Tensor:
@@ -470,6 +493,7 @@ __all__ = [
     "pick_num_splits",
     "decode_partials",
     "split_reduce",
+    "flat_merge",
     "split_count_for",
     "plan_num_splits",
     "plan_decode",

@@ -156,3 +156,20 @@ def test_flat_occupancy_query(kv_dtype, scale_dtype, d):
     assert 1 <= n <= 8
     if d == 128:
         assert n == _FLAT_WGS_FALLBACK[(2 if kv_dtype in ("fp16", "bf16") else 1, d)]
+
+
+def test_flat_partials_then_merge_equals_decode():
+    """pa_decode_partials + pa_flat_merge is pa_decode, bit for bit."""
+    from pagedattn.hip_decode import flat_merge
+
+    q, c = _case(LLAMA3_8B, RAGGED, seed=9)
+    flat = 29
+    b, hq, d = q.shape
+    want = paged_decode_hip(q, c, flat_splits=flat).clone()
+    part = torch.empty((b + flat, hq, d), dtype=torch.float32, device="cuda")
+    lse = torch.empty((b + flat, hq), dtype=torch.float32, device="cuda")
+    out = torch.full_like(q, 3.0)
+    decode_partials(q, c, 1, part_out=part, part_lse=lse, flat_splits=flat, out=out)
+    flat_merge(q, c, flat, part, lse, out)
+    torch.cuda.synchronize()
+    assert torch.equal(out, want)

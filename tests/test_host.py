@@ -368,3 +368,11 @@ def test_flat_occupancy_query_validates_before_hip():
     assert lib.pa_flat_workgroups_per_cu(_abi.PA_KV_FP16, _abi.PA_SCALE_NONE, 128, None) \
         == _abi.PA_ERR_INVALID
     assert lib.pa_last_error().decode()
+
+
+@cpu_only
+def test_flat_merge_needs_flat_splits():
+    lib = _lib()
+    a = _valid_args(part_out=FAKE, part_lse=FAKE, stride_pb=32 * 128, stride_ph=128)
+    assert lib.pa_flat_merge(ctypes.byref(a), None) == _abi.PA_ERR_INVALID
+    assert "flat_splits" in lib.pa_last_error().decode()
