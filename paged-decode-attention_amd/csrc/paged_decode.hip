@@ -75,6 +75,11 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr uint32_t kInt8Sign = 0x80808080u;      // int8 x -> x + 128 in every byte
 constexpr uint32_t kInt8PairSign = 0x00800080u;  // the same for [b, 0, b', 0]
 constexpr float kInt8Unit = 16777216.0f;      // 2^24: int8 operands are (x + 128) * 2^-24
+// s_waitcnt immediate (gfx9 encoding): vmcnt(0), expcnt and lgkmcnt at their maxima
+constexpr int kWaitVmcnt0 = 0x0F70;
+// A flat-split wave with at most this many tiles keeps two tiles in flight:
+// short ranges are latency-bound; longer ones stream faster with one.
+constexpr int kDeepTiles = 16;
 
 struct KParams {
   const uint8_t *q;
@@ -234,6 +239,14 @@ __device__ __forceinline__ float load_scale(const uint8_t *p) {
   }
 }
 
+// Block tables and lengths are read-only for a whole launch. Reading them
+// through the constant address space lets the compiler use scalar loads for
+// the wave-uniform reads even in kernels that store inside their tile loop;
+// a scalar load's wait (lgkmcnt) never holds back the K/V loads in flight,
+// where a vector load's (vmcnt) would wait for them.
+typedef __attribute__((address_space(4))) const int32_t ro_i32;
+__device__ __forceinline__ const ro_i32 *ro(const int32_t *ptr) { return (const ro_i32 *)ptr; }
+
 // Compile-time geometry for one (KV dtype, head_dim) instance.
 //
 // K is fetched in whole rows: consecutive lanes read consecutive 16-byte
@@ -310,9 +323,12 @@ __device__ __forceinline__ void remove_offsets(WaveState<KV, D> &st) {
 // Issue the loads of the tile starting at token n0 (< hi). Rows at or past
 // `hi` in the last tile are clamped to valid rows of the sequence: they are
 // read (finite data) and masked out of the softmax by compute_tile.
+// With `wait_prev`, the K/V loads are issued only once the loads issued
+// before them (the tile about to be computed) have arrived: one tile in
+// flight per wave instead of two (the block-table reads still go ahead).
 template <int KV, int SC, int D>
-__device__ __forceinline__ void load_tile(Tile<KV, D> &r, const KParams &p, const int32_t *bt_row,
-                                          int kvh, int n0, int hi, int lane) {
+__device__ __forceinline__ void load_tile(Tile<KV, D> &r, const KParams &p, const ro_i32 *bt_row,
+                                          int kvh, int n0, int hi, int lane, bool wait_prev = false) {
   using G = Geo<KV, D>;
   constexpr int NS = G::kNSub;
   const int r16 = lane & 15;
@@ -325,14 +341,16 @@ __device__ __forceinline__ void load_tile(Tile<KV, D> &r, const KParams &p, cons
   int phys[NS], off[NS];
 #pragma unroll
   for (int u = 0; u < NS; ++u) {
-    int t0 = n0 + 16 * u;
-    if (tail) t0 = min(t0, (hi - 1) & ~15);  // a sub-tile past the end re-reads the last one
+    // a sub-tile past the end re-reads the last one (a no-op before the tail:
+    // n0 is a multiple of 32 and (hi - 1) & ~15 >= n0 + 16 there)
+    const int t0 = min(n0 + 16 * u, (hi - 1) & ~15);
     phys[u] = min(max(bt_row[t0 >> p.log2_page], 0), p.num_blocks - 1);
     off[u] = t0 & page_mask;
     lim[u] = hi - 1 - t0;  // last valid row of the sub-tile (>= 15 unless tail)
     base[u] = (int64_t)phys[u] * p.skn + (int64_t)off[u] * p.skt + (int64_t)kvh * p.skh;
   }
   const uint32_t skt = (uint32_t)p.skt;
+  if (wait_prev) __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
 
 #pragma unroll
   for (int i = 0; i < G::kKLoads; ++i) {
@@ -800,7 +818,7 @@ paged_decode_kernel(const KParams p) {
   reset_state(st);
   load_q(st, p, b, qh0, nh, r16, c);
 
-  const int32_t *bt_row = p.bt + (int64_t)b * p.sbtb;
+  const ro_i32 *bt_row = ro(p.bt) + (int64_t)b * p.sbtb;
   float *sc_lds = sm_sc[wave];
   uint8_t *k_lds = sm_raw + wave * G::kKSlotBytes;
   const int ntiles = (hi > lo) ? (hi - lo + G::kTT - 1) / G::kTT : 0;
@@ -899,7 +917,7 @@ paged_decode_kernel(const KParams p) {
 // ----------------------------------------------------------------------------
 
 // Tiles of sequence b (its length clamped to the block table).
-__device__ __forceinline__ int seq_tiles(const int32_t *seq_lens, int b, int max_tokens) {
+__device__ __forceinline__ int seq_tiles(const ro_i32 *seq_lens, int b, int max_tokens) {
   const int t = max(0, min(seq_lens[b], max_tokens));
   return (t + kSplitAlign - 1) / kSplitAlign;
 }
@@ -919,13 +937,16 @@ __device__ __forceinline__ int wave_incl_scan(int x, int lane) {
   return x;
 }
 
-// Total flat tiles of the batch (wave-uniform).
-__device__ __forceinline__ int flat_total(const int32_t *seq_lens, int batch, int max_tokens,
-                                          int lane) {
+// Total flat tiles of the batch (wave-uniform); `len0` receives this lane's
+// clamped length of sequence `lane` (0 past the batch).
+__device__ __forceinline__ int flat_total(const ro_i32 *seq_lens, int batch, int max_tokens,
+                                          int lane, int &len0) {
   int total = 0;
   for (int base = 0; base < batch; base += 64) {
     const int b = base + lane;
-    total += wave_sum(b < batch ? seq_tiles(seq_lens, b, max_tokens) : 0);
+    const int len = b < batch ? max(0, min(seq_lens[b], max_tokens)) : 0;
+    if (base == 0) len0 = len;
+    total += wave_sum((len + kSplitAlign - 1) / kSplitAlign);
   }
   return __builtin_amdgcn_readfirstlane(total);
 }
@@ -937,33 +958,38 @@ struct SeqCursor {
 };
 
 // The sequence holding flat tile f (< total) and f's tile index in it.
-__device__ __forceinline__ SeqCursor flat_locate(const int32_t *seq_lens, int batch, int max_tokens,
-                                                 int f, int lane) {
+// `len0` is this lane's clamped length of sequence `lane` (batch <= 64: the
+// values flat_start already loaded), or -1 to load them again.
+__device__ __forceinline__ SeqCursor flat_locate(const ro_i32 *seq_lens, int batch, int max_tokens,
+                                                 int f, int lane, int len0) {
   SeqCursor cur = {0, 0, 0, 0};
   int run = 0;
   for (int base = 0; base < batch; base += 64) {
     const int b = base + lane;
-    const int t = b < batch ? seq_tiles(seq_lens, b, max_tokens) : 0;
+    const int len = (base == 0 && len0 >= 0) ? len0
+                    : b < batch ? max(0, min(seq_lens[b], max_tokens)) : 0;
+    const int t = (len + kSplitAlign - 1) / kSplitAlign;
     const int incl = wave_incl_scan(t, lane) + run;
     const uint64_t hit = __builtin_amdgcn_ballot_w64(incl > f);
     if (hit != 0) {
       const int l = __builtin_ctzll(hit);
       cur.b = base + l;
       cur.t = f - __shfl(incl - t, l);
+      cur.len = __shfl(len, l);
       break;
     }
     run = __shfl(incl, 63);
   }
   cur.b = __builtin_amdgcn_readfirstlane(cur.b);
   cur.t = __builtin_amdgcn_readfirstlane(cur.t);
-  cur.len = __builtin_amdgcn_readfirstlane(max(0, min(seq_lens[cur.b], max_tokens)));
+  cur.len = __builtin_amdgcn_readfirstlane(cur.len);
   cur.tiles = (cur.len + kSplitAlign - 1) / kSplitAlign;
   return cur;
 }
 
 // Step to the next flat tile. Only called while the range has another tile,
 // so a non-empty sequence follows; the batch bound only guards the reads.
-__device__ __forceinline__ void cursor_next(SeqCursor &cur, const int32_t *seq_lens, int batch,
+__device__ __forceinline__ void cursor_next(SeqCursor &cur, const ro_i32 *seq_lens, int batch,
                                             int max_tokens) {
   if (++cur.t < cur.tiles) return;
   cur.t = 0;
@@ -1009,13 +1035,15 @@ paged_decode_flat_kernel(const KParams p) {
   const int qh0 = kvh * p.group + ht * 16;
   const int nh = min(16, p.group - ht * 16);
 
-  const int total = flat_total(p.seq_lens, p.batch, p.max_tokens, lane);
+  int len0 = 0;
+  const int total = flat_total(ro(p.seq_lens), p.batch, p.max_tokens, lane, len0);
   const int per = max(1, (total + p.flat_splits - 1) / p.flat_splits);
   const int r0 = j * per;
   if (r0 >= total) return;
   const int n = min(per, total - r0);  // this wave's tiles
 
-  SeqCursor cc = flat_locate(p.seq_lens, p.batch, p.max_tokens, r0, lane);  // compute cursor
+  // compute cursor (one pass over seq_lens when the batch fits one wave)
+  SeqCursor cc = flat_locate(ro(p.seq_lens), p.batch, p.max_tokens, r0, lane, p.batch <= 64 ? len0 : -1);
   SeqCursor lc = cc;                                                        // load cursor
   int seg_t0 = cc.t;  // first tile of the current segment
 
@@ -1026,7 +1054,7 @@ paged_decode_flat_kernel(const KParams p) {
   float *sc_lds = sm_sc[wave];
   uint8_t *k_lds = sm_k + wave * G::kKSlotBytes;
 
-  auto bt_of = [&](int b) { return p.bt + (int64_t)b * p.sbtb; };
+  auto bt_of = [&](int b) { return ro(p.bt) + (int64_t)b * p.sbtb; };
   // After computing the wave's i-th tile: close the segment at a sequence
   // end or at the end of the range, then move the compute cursor on.
   auto post = [&](int i) {
@@ -1041,7 +1069,7 @@ paged_decode_flat_kernel(const KParams p) {
                      (int64_t)slot * p.spb, (int64_t)slot * p.slb);
       }
       if (i + 1 < n) {
-        cursor_next(cc, p.seq_lens, p.batch, p.max_tokens);
+        cursor_next(cc, ro(p.seq_lens), p.batch, p.max_tokens);
         seg_t0 = 0;
         reset_state(st);
         load_q(st, p, cc.b, qh0, nh, r16, c);
@@ -1053,22 +1081,23 @@ paged_decode_flat_kernel(const KParams p) {
   auto n0_of = [](const SeqCursor &cur) { return cur.t * G::kTT; };
 
   if constexpr (G::kPrefetch) {
+    const bool shallow = n > kDeepTiles;
     Tile<KV, D> ta, tb;
     load_tile<KV, SC, D>(ta, p, bt_of(lc.b), kvh, n0_of(lc), lc.len, lane);
     int i = 0;
     for (; i + 2 < n; i += 2) {
-      cursor_next(lc, p.seq_lens, p.batch, p.max_tokens);
-      load_tile<KV, SC, D>(tb, p, bt_of(lc.b), kvh, n0_of(lc), lc.len, lane);
+      cursor_next(lc, ro(p.seq_lens), p.batch, p.max_tokens);
+      load_tile<KV, SC, D>(tb, p, bt_of(lc.b), kvh, n0_of(lc), lc.len, lane, shallow);
       compute_tile<KV, SC, D>(st, ta, p, n0_of(cc), cc.len, lane, sc_lds, k_lds);
       post(i);
-      cursor_next(lc, p.seq_lens, p.batch, p.max_tokens);
-      load_tile<KV, SC, D>(ta, p, bt_of(lc.b), kvh, n0_of(lc), lc.len, lane);
+      cursor_next(lc, ro(p.seq_lens), p.batch, p.max_tokens);
+      load_tile<KV, SC, D>(ta, p, bt_of(lc.b), kvh, n0_of(lc), lc.len, lane, shallow);
       compute_tile<KV, SC, D>(st, tb, p, n0_of(cc), cc.len, lane, sc_lds, k_lds);
       post(i + 1);
     }
     if (i + 1 < n) {
-      cursor_next(lc, p.seq_lens, p.batch, p.max_tokens);
-      load_tile<KV, SC, D>(tb, p, bt_of(lc.b), kvh, n0_of(lc), lc.len, lane);
+      cursor_next(lc, ro(p.seq_lens), p.batch, p.max_tokens);
+      load_tile<KV, SC, D>(tb, p, bt_of(lc.b), kvh, n0_of(lc), lc.len, lane, shallow);
       compute_tile<KV, SC, D>(st, ta, p, n0_of(cc), cc.len, lane, sc_lds, k_lds);
       post(i);
       compute_tile<KV, SC, D>(st, tb, p, n0_of(cc), cc.len, lane, sc_lds, k_lds);
@@ -1124,12 +1153,19 @@ __device__ __forceinline__ void write_merged(const RParams &p, const float *acc,
 //               empty sequences get zeros
 enum { kMergeAll = 0, kMergeAuto = 1, kMergeFlat = 2 };
 
+// kMergeWaves waves per workgroup, one (b, h) each; the waves never
+// synchronise with each other (each stages its weights in its own LDS row).
+constexpr int kMergeWaves = 1;
+
 template <int D, int KIND>
-__global__ void __launch_bounds__(64) split_reduce_kernel(const RParams p) {
+__global__ void __launch_bounds__(kMergeWaves * 64) split_reduce_kernel(const RParams p) {
   constexpr int kPer = D / 64 > 0 ? D / 64 : 1;  // head-dim elements per lane
-  __shared__ float sw[kReduceChunk];
-  const int lane = threadIdx.x;
-  const int bh = blockIdx.x;
+  __shared__ float sw_all[kMergeWaves][kReduceChunk];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  float *sw = sw_all[wave];
+  const int bh = blockIdx.x * kMergeWaves + wave;
+  if (bh >= p.batch * p.num_heads) return;
   const int b = bh / p.num_heads;
   const int h = bh % p.num_heads;
   const float *lse = p.part_lse + (int64_t)b * p.slb + (int64_t)h * p.slh;
@@ -1146,11 +1182,11 @@ __global__ void __launch_bounds__(64) split_reduce_kernel(const RParams p) {
     int total = 0, cu = 0;
     for (int base = 0; base < p.batch; base += 64) {
       const int bb = base + lane;
-      const int t = bb < p.batch ? seq_tiles(p.seq_lens, bb, p.max_tokens) : 0;
+      const int t = bb < p.batch ? seq_tiles(ro(p.seq_lens), bb, p.max_tokens) : 0;
       total += wave_sum(t);
       cu += wave_sum(bb < b ? t : 0);
     }
-    const int nt = seq_tiles(p.seq_lens, b, p.max_tokens);
+    const int nt = seq_tiles(ro(p.seq_lens), b, p.max_tokens);
     S = 0;  // empty sequence: the merge below writes zeros
     if (nt > 0) {
       const int per = max(1, (total + p.num_splits - 1) / p.num_splits);
@@ -1212,14 +1248,18 @@ __global__ void __launch_bounds__(64) split_reduce_kernel(const RParams p) {
   // lane-local partial sums of the weights, combined in a fixed tree below
   for (int s0 = 0; s0 < S; s0 += kReduceChunk) {
     const int n = min(kReduceChunk, S - s0);
-    __syncthreads();
+    // the previous chunk's weights are read before they are overwritten
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
     for (int s = lane; s < n; s += 64) {
       const float ls = lse[(s0 + s) * lse_step];
       const float w = (ls == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ls - m);
       sw[s] = w;
       wsum += w;
     }
-    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     if (active && m != -INFINITY) {
       const float *src = part + (int64_t)s0 * part_step + lane * kPer;
       int s = 0;
@@ -1479,12 +1519,13 @@ int check_reduce(const pa_reduce_args *r, RParams *rp) {
 
 template <int KIND>
 hipError_t launch_reduce(const RParams &rp, int batch, int d, hipStream_t st) {
-  const int grid = batch * rp.num_heads;
+  const int grid = (batch * rp.num_heads + kMergeWaves - 1) / kMergeWaves;
+  const dim3 blk(kMergeWaves * 64);
   switch (d) {
-    case 32: hipLaunchKernelGGL((split_reduce_kernel<32, KIND>), dim3(grid), dim3(64), 0, st, rp); break;
-    case 64: hipLaunchKernelGGL((split_reduce_kernel<64, KIND>), dim3(grid), dim3(64), 0, st, rp); break;
-    case 128: hipLaunchKernelGGL((split_reduce_kernel<128, KIND>), dim3(grid), dim3(64), 0, st, rp); break;
-    default: hipLaunchKernelGGL((split_reduce_kernel<256, KIND>), dim3(grid), dim3(64), 0, st, rp); break;
+    case 32: hipLaunchKernelGGL((split_reduce_kernel<32, KIND>), dim3(grid), blk, 0, st, rp); break;
+    case 64: hipLaunchKernelGGL((split_reduce_kernel<64, KIND>), dim3(grid), blk, 0, st, rp); break;
+    case 128: hipLaunchKernelGGL((split_reduce_kernel<128, KIND>), dim3(grid), blk, 0, st, rp); break;
+    default: hipLaunchKernelGGL((split_reduce_kernel<256, KIND>), dim3(grid), blk, 0, st, rp); break;
   }
   return hipGetLastError();
 }

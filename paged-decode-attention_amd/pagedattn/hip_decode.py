@@ -37,10 +37,13 @@ MIN_SPLIT_TOKENS = 512
 # the BASELINE ragged / long-context shapes: 2 beats 1 and 3).
 SPLIT_ROUNDS = 2
 
-# Flat split: one round of resident waves (a second round measured slower on
-# every BASELINE shape), used when each wave gets at least this many
-# 32-token tiles; below that the batch is too small for it (latency-bound
-# decodes run faster unsplit).
+# Flat split: one round of waves, at most FLAT_WAVES_PER_SIMD per SIMD even
+# where the registers allow more (1-byte KV fits 3): two streaming waves per
+# SIMD measured fastest on every BASELINE split shape (C4 171 us at 2, 183 at
+# 3; a second round or an uneven 2.5 per SIMD is slower still). Used when
+# each wave gets at least MIN_FLAT_TILES_PER_WAVE 32-token tiles; smaller
+# batches are latency-bound and run faster unsplit.
+FLAT_WAVES_PER_SIMD = 2
 MIN_FLAT_TILES_PER_WAVE = 4
 # Workgroups of the flat kernel per CU when the library cannot be asked (no
 # GPU): register-limited occupancy of the gfx950 build by (bytes per stored
@@ -111,9 +114,12 @@ def plan_num_splits(seq_lens, num_kv_heads: int, group: int, sm_count: int) -> t
 
 
 def flat_splits_for(num_kv_heads: int, group: int, sm_count: int, workgroups_per_cu: int) -> int:
-    """One round of resident waves over the (kv head, head tile) units."""
+    """One round of waves over the (kv head, head tile) units: as many as
+    the CUs hold (4 SIMDs each, `workgroups_per_cu` waves per SIMD), capped at
+    FLAT_WAVES_PER_SIMD per SIMD."""
     units = num_kv_heads * -(-group // _abi.PA_MAX_GROUP)
-    waves = max(1, sm_count) * WAVES_PER_WORKGROUP * max(1, workgroups_per_cu)
+    per_simd = max(1, min(workgroups_per_cu, FLAT_WAVES_PER_SIMD))
+    waves = max(1, sm_count) * WAVES_PER_WORKGROUP * per_simd
     return int(max(1, min(waves // units, _abi.PA_MAX_FLAT_SPLITS)))
 
 

@@ -335,14 +335,15 @@ def test_plan_num_splits():
 def test_flat_splits_for_and_plan_decode():
     from pagedattn import flat_splits_for, plan_decode
 
-    # one round of resident waves over the (kv head, head tile) units
-    assert flat_splits_for(8, 4, 256, 3) == 384
+    # one round of waves over the (kv head, head tile) units, at most two per SIMD
     assert flat_splits_for(8, 4, 256, 2) == 256
+    assert flat_splits_for(8, 4, 256, 3) == 256
+    assert flat_splits_for(8, 4, 256, 1) == 128
     assert flat_splits_for(2, 20, 256, 2) == 512      # group 20: two head tiles
     assert flat_splits_for(64, 1, 4, 1) == 1
     # every BASELINE split shape takes the flat split ...
     assert plan_decode([4096] * 64, 8, 4, 256, 2) == (1, 4096, 256)
-    assert plan_decode([16384] * 32, 8, 8, 256, 3) == (1, 16384, 384)
+    assert plan_decode([16384] * 32, 8, 8, 256, 3) == (1, 16384, 256)
     assert plan_decode([131072] * 4, 8, 4, 256, 2) == (1, 131072, 256)
     # ... and a latency-bound batch (too few tiles per wave) the classic path
     s, m, f = plan_decode([192] * 24, 2, 7, 256, 4)
