@@ -942,6 +942,7 @@ __device__ __forceinline__ int wave_incl_scan(int x, int lane) {
 __device__ __forceinline__ int flat_total(const ro_i32 *seq_lens, int batch, int max_tokens,
                                           int lane, int &len0) {
   int total = 0;
+#pragma unroll 4
   for (int base = 0; base < batch; base += 64) {
     const int b = base + lane;
     const int len = b < batch ? max(0, min(seq_lens[b], max_tokens)) : 0;
@@ -1180,6 +1181,7 @@ __global__ void __launch_bounds__(kMergeWaves * 64) split_reduce_kernel(const RP
   } else if (KIND == kMergeFlat) {
     // the decode's ranges: per = ceil(total / F) flat tiles each
     int total = 0, cu = 0;
+#pragma unroll 4
     for (int base = 0; base < p.batch; base += 64) {
       const int bb = base + lane;
       const int t = bb < p.batch ? seq_tiles(ro(p.seq_lens), bb, p.max_tokens) : 0;

@@ -41,6 +41,7 @@ if str(_PKG_ROOT) not in sys.path:
 from pagedattn.cache import PagedKVCache  # noqa: E402
 from pagedattn.config import ModelShape  # noqa: E402
 from pagedattn.hip_decode import (  # noqa: E402
+    FLAT_MAX_BATCH,
     MIN_FLAT_TILES_PER_WAVE,
     TILE_TOKENS,
     flat_splits_for,
@@ -167,7 +168,7 @@ def decode_forward(impl, layer, query, key, value, kv_cache, attn_metadata, outp
     group = impl.num_heads // impl.num_kv_heads
     flat = flat_splits_for(impl.num_kv_heads, group, _cu_count(query.device),
                            flat_workgroups_per_cu(cache.kv_dtype, impl.head_size))
-    if n * -(-msl // TILE_TOKENS) >= MIN_FLAT_TILES_PER_WAVE * flat:
+    if n <= FLAT_MAX_BATCH and n * -(-msl // TILE_TOKENS) >= MIN_FLAT_TILES_PER_WAVE * flat:
         decode(query[:n], cache, out=output[:n], sm_scale=impl.scale, flat_splits=flat)
     else:
         splits = pick_num_splits(n, impl.num_kv_heads, msl, _cu_count(query.device))

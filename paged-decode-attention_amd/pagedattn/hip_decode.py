@@ -45,6 +45,10 @@ SPLIT_ROUNDS = 2
 # batches are latency-bound and run faster unsplit.
 FLAT_WAVES_PER_SIMD = 2
 MIN_FLAT_TILES_PER_WAVE = 4
+# Every flat wave (and every merge wave) scans seq_lens once, batch / 64
+# loads per lane: above this batch the classic split is used instead (such
+# batches fill the GPU unsplit anyway).
+FLAT_MAX_BATCH = 512
 # Workgroups of the flat kernel per CU when the library cannot be asked (no
 # GPU): register-limited occupancy of the gfx950 build by (bytes per stored
 # element, head_dim).
@@ -127,8 +131,9 @@ def plan_decode(seq_lens, num_kv_heads: int, group: int, sm_count: int,
                 workgroups_per_cu: int = 2) -> tuple[int, int, int]:
     """(num_splits, max_seq_len, flat_splits) for a batch whose lengths the host knows.
 
-    The flat split (one round of resident waves, `flat_splits_for`) whenever
-    each of its waves gets at least MIN_FLAT_TILES_PER_WAVE tiles: it is
+    The flat split (one round of waves, `flat_splits_for`) whenever each of
+    its waves gets at least MIN_FLAT_TILES_PER_WAVE tiles and the batch is at
+    most FLAT_MAX_BATCH: it is
     balanced for any mix of lengths and measured fastest on every BASELINE
     split shape. Smaller batches take `plan_num_splits`.
     """
@@ -136,7 +141,7 @@ def plan_decode(seq_lens, num_kv_heads: int, group: int, sm_count: int,
     tmax = max(lens) if lens else 0
     flat = flat_splits_for(num_kv_heads, group, sm_count, workgroups_per_cu)
     tiles = sum(-(-t // TILE_TOKENS) for t in lens)
-    if tiles >= MIN_FLAT_TILES_PER_WAVE * flat:
+    if len(lens) <= FLAT_MAX_BATCH and tiles >= MIN_FLAT_TILES_PER_WAVE * flat:
         return 1, tmax, flat
     splits, tmax = plan_num_splits(lens, num_kv_heads, group, sm_count)
     return splits, tmax, 0

@@ -173,3 +173,17 @@ def test_flat_partials_then_merge_equals_decode():
     flat_merge(q, c, flat, part, lse, out)
     torch.cuda.synchronize()
     assert torch.equal(out, want)
+
+
+@pytest.mark.parametrize("batch,flat", [(130, 37), (300, 256)])
+def test_flat_batches_above_one_wave(batch, flat):
+    """Batches above 64 sequences: the range locate and the merge scan
+    seq_lens in several 64-lane chunks (and the locate takes its second pass)."""
+    g = torch.Generator().manual_seed(batch)
+    lens = torch.randint(0, 700, (batch,), generator=g).tolist()
+    lens[5] = 0
+    lens[64] = 1
+    lens[-1] = 0
+    shape = ModelShape(8, 2, 64, "b")
+    q, c = _case(shape, lens, seed=10)
+    _check(q, c, flat)

@@ -349,6 +349,10 @@ def test_flat_splits_for_and_plan_decode():
     s, m, f = plan_decode([192] * 24, 2, 7, 256, 4)
     assert f == 0 and s >= 1 and m == 192
     assert plan_decode([], 8, 4, 256) == (1, 0, 0)
+    # batches above FLAT_MAX_BATCH take the classic planner
+    from pagedattn.hip_decode import FLAT_MAX_BATCH
+    assert plan_decode([4096] * (FLAT_MAX_BATCH + 1), 8, 4, 256, 2)[2] == 0
+    assert plan_decode([4096] * FLAT_MAX_BATCH, 8, 4, 256, 2)[2] == 256
     # the threshold: MIN_FLAT_TILES_PER_WAVE tiles per wave
     from pagedattn.hip_decode import MIN_FLAT_TILES_PER_WAVE
     f = flat_splits_for(1, 1, 1, 1)
