@@ -1002,10 +1002,11 @@ __device__ __forceinline__ void cursor_next(SeqCursor &cur, const ro_i32 *seq_le
   }
 }
 
-// 1-byte KV at head_dim <= 128 fits three workgroups per CU.
+// Built for two waves per SIMD, the count the flat split launches (more
+// streaming waves measured slower); 1-byte KV at head_dim 128 would fit
+// three, and the looser register budget measured marginally faster.
 template <int KV, int SC, int D>
-__global__ void __launch_bounds__(kWaves * 64)
-__attribute__((amdgpu_waves_per_eu(Geo<KV, D>::kElem == 1 && D <= 128 ? 3 : 2)))
+__global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
 paged_decode_flat_kernel(const KParams p) {
   using G = Geo<KV, D>;
   static_assert(G::kTT == kSplitAlign, "flat tiles are the kernel's tiles");

@@ -147,15 +147,15 @@ def test_flat_partial_slots_match_oracle(flat):
                                                   ("int8", torch.float16), ("int8", torch.float32)])
 @pytest.mark.parametrize("d", [32, 64, 128, 256])
 def test_flat_occupancy_query(kv_dtype, scale_dtype, d):
-    """The library's occupancy answer sizes flat_splits; at head_dim 128 (the
-    BASELINE shapes) it must equal the no-GPU fallback table."""
-    from pagedattn.hip_decode import _FLAT_WGS_FALLBACK, flat_workgroups_per_cu
+    """The library's occupancy answer sizes flat_splits; the size it gives
+    must equal the one the no-GPU fallback table gives."""
+    from pagedattn.hip_decode import _FLAT_WGS_FALLBACK, flat_splits_for, flat_workgroups_per_cu
 
     n = flat_workgroups_per_cu(kv_dtype, d, scale_dtype)
     print(f"{kv_dtype} d={d}: {n} workgroups/CU")
     assert 1 <= n <= 8
-    if d == 128:
-        assert n == _FLAT_WGS_FALLBACK[(2 if kv_dtype in ("fp16", "bf16") else 1, d)]
+    table = _FLAT_WGS_FALLBACK[(2 if kv_dtype in ("fp16", "bf16") else 1, d)]
+    assert flat_splits_for(8, 4, 256, n) == flat_splits_for(8, 4, 256, table)
 
 
 def test_flat_partials_then_merge_equals_decode():
