@@ -119,3 +119,33 @@ def test_impl_forward_bf16_cache():
     want = oracle.reference_decode(query, c, out_dtype=torch.float32)
     err = (output.float().cpu() - want).abs()
     assert bool((err <= 2e-3 + 2.0 ** -8 * want.abs()).all())
+
+
+def test_impl_forward_large_step_takes_the_flat_split(monkeypatch):
+    """A step big enough for the flat split (n * ceil(max_seq_len / 32) tiles
+    reach the planner's threshold) through the boundary, vs the oracle."""
+    _, Impl = vb.build_backend_classes(object, _BaseImpl)
+    g = torch.Generator().manual_seed(35)
+    lens = torch.randint(1, 2049, (16,), generator=g).tolist()
+    lens[3] = 2048
+    n = len(lens)
+    c = allocate(LLAMA3_8B, n, lens, seed=35, device="cuda")
+    kv_cache = torch.stack([c.k_cache, c.v_cache])
+    meta = types.SimpleNamespace(max_query_len=1, num_actual_tokens=n, use_cascade=False,
+                                 local_attn_metadata=None, max_seq_len=max(lens),
+                                 block_table=c.block_table, seq_lens=c.seq_lens, slot_mapping=None)
+    query = seeded_q(n, 32, 128, 35, device="cuda")
+    output = torch.zeros_like(query)
+    flat_calls = []
+    real_forward, real_decode = vb.decode_forward, vb.paged_decode_triton
+
+    def spy(*a, **kw):
+        flat_calls.append(kw.get("flat_splits"))
+        return real_decode(*a, **kw)
+
+    monkeypatch.setattr(vb, "decode_forward", lambda *a, **kw: real_forward(*a, decode=spy, **kw))
+    Impl(LLAMA3_8B).forward(None, query, None, None, kv_cache, meta, output)
+    torch.cuda.synchronize()
+    assert flat_calls and flat_calls[0]
+    want = oracle.reference_decode(query, c, out_dtype=torch.float32)
+    assert max_abs(output, want) < 2e-3

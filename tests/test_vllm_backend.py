@@ -181,3 +181,28 @@ def test_qualname_resolves():
     mod = importlib.import_module(mod_name)
     assert mod is vb and hasattr(mod, cls_name)
     assert (mod.PagedAttnTritonBackend is None) == (not vb.HAVE_VLLM)
+
+
+def test_decode_forward_takes_the_flat_split_for_large_batches(monkeypatch):
+    """Host-side routing only: with n * ceil(max_seq_len / 32) tiles enough
+    for the flat split's waves, the step launches it (no device sync)."""
+    monkeypatch.setattr(vb, "_cu_count", lambda dev: 256)
+    monkeypatch.setattr(vb, "flat_workgroups_per_cu", lambda kv, d: 2)
+    calls = []
+
+    def fake_decode(q, cache, out, sm_scale, **kw):
+        calls.append(kw)
+
+    impl = FakeBaseImpl()
+    n = 64
+    q = torch.randn(n, 32, 128).half()
+    meta = _meta(num_actual_tokens=n, max_seq_len=4096,
+                 block_table=torch.zeros((n, 256), dtype=torch.int32),
+                 seq_lens=torch.full((n,), 4096, dtype=torch.int32))
+    impl.kv_sharing_target_layer_name = "shared"
+    vb.decode_forward(impl, None, q, q, q, _kv(), meta, torch.zeros_like(q), decode=fake_decode)
+    assert calls[-1] == {"flat_splits": vb.flat_splits_for(8, 4, 256, 2)}
+    # a small step stays on the classic split
+    meta = _meta(max_seq_len=300)
+    vb.decode_forward(impl, None, q, q, q, _kv(), meta, torch.zeros_like(q), decode=fake_decode)
+    assert calls[-1] == {"num_splits": vb.pick_num_splits(2, 8, 300, 256), "max_seq_len": 300}
