@@ -254,7 +254,7 @@ def main() -> int:
 
     import torch
 
-    from pagedattn import allocate, flat_workgroups_per_cu, plan_decode, plan_num_splits
+    from pagedattn import allocate, flat_waves_per_simd, plan_decode, plan_num_splits
     from pagedattn.hip_decode import _WS, _cu_count, decode_partials, paged_decode_hip
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
@@ -289,9 +289,9 @@ def main() -> int:
     cus = _cu_count(dev)
     # the workload's lengths are known here, so the exact planner decides
     # unless --splits / --flat force a launch shape
-    wgs = flat_workgroups_per_cu(wl.kv_dtype, shape.head_dim,
+    wps = flat_waves_per_simd(wl.kv_dtype, shape.head_dim,
                                  torch.float32 if wl.scale_fp32 else torch.float16)
-    splits, _, flat = plan_decode(wl.lens, shape.num_kv_heads, shape.gqa_group, cus, wgs)
+    splits, _, flat = plan_decode(wl.lens, shape.num_kv_heads, shape.gqa_group, cus, wps)
     if args.flat is not None or args.splits:
         flat = int(args.flat or 0)
         splits = 1 if flat else (args.splits or

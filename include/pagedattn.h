@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define PA_ABI_VERSION 3
+#define PA_ABI_VERSION 4
 
 /* Return codes. */
 #define PA_OK 0
@@ -222,14 +222,15 @@ int pa_cache_write(const pa_cache_write_args *args, void *stream);
  * (pagedattn/triton_decode.py:368-376) for the flat split. */
 int pa_flat_merge(const pa_decode_args *args, void *stream);
 
-/* Workgroups of the flat decode kernel for (kv_dtype, scale_dtype,
- * head_dim) that one CU holds at once (hipOccupancyMaxActiveBlocksPerMultiprocessor
- * on the current device), written to *out. A host planner sizes
- * flat_splits from it: one round of resident waves is
- * CUs * 4 * (*out) waves over num_kv_heads * ceil(group / 16) units.
- * No counterpart in the reference (its split count comes from the SM count
- * alone, pagedattn/triton_decode.py:248-263). */
-int pa_flat_workgroups_per_cu(int kv_dtype, int scale_dtype, int head_dim, int *out);
+/* Waves of the flat decode kernel for (kv_dtype, scale_dtype, head_dim)
+ * that one SIMD holds at once (hipOccupancyMaxActiveBlocksPerMultiprocessor
+ * on the current device, times the kernel's workgroup width, over the 4
+ * SIMDs of a CU), written to *out. A host planner sizes flat_splits from
+ * it: one round of waves is CUs * 4 * min(*out, 2) waves over
+ * num_kv_heads * ceil(group / 16) units. No counterpart in the reference
+ * (its split count comes from the SM count alone,
+ * pagedattn/triton_decode.py:248-263). */
+int pa_flat_waves_per_simd(int kv_dtype, int scale_dtype, int head_dim, int *out);
 
 /* Message for the last non-zero return on the calling thread ("" if none). */
 const char *pa_last_error(void);

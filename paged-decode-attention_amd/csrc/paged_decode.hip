@@ -68,7 +68,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kWaves = 4;          // waves per workgroup
+constexpr int kWaves = 4;          // waves per workgroup (unsplit / classic split)
+constexpr int kMaxFlatWaves = 8;   // the widest flat-kernel workgroup
 constexpr int kSplitAlign = 32;    // split ranges are multiples of this many tokens
 constexpr float kRescaleLog2 = 8.0f;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -281,6 +282,10 @@ struct Geo {
   // largest instance that measured best double-buffered: fp16 at D = 128)
   static constexpr int kTileWords = 4 * kKLoads + kVRows * kVWords;
   static constexpr bool kPrefetch = 2 * kTileWords + 4 * kE + 4 * kKSteps <= 176;
+  // Flat-kernel workgroup: one wave per neighbouring kv head, enough of them
+  // that a workgroup reads about 1 KB of every token row of a page at once
+  // (4 heads of 256-B rows, 8 of 128-B rows), the width measured fastest.
+  static constexpr int kFlatWaves = kRowBytes <= 128 ? 8 : 4;
 };
 
 // Registers of one tile of one wave.
@@ -1006,12 +1011,13 @@ __device__ __forceinline__ void cursor_next(SeqCursor &cur, const ro_i32 *seq_le
 // streaming waves measured slower); 1-byte KV at head_dim 128 would fit
 // three, and the looser register budget measured marginally faster.
 template <int KV, int SC, int D>
-__global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ void __launch_bounds__((Geo<KV, D>::kFlatWaves * 64)) __attribute__((amdgpu_waves_per_eu(2)))
 paged_decode_flat_kernel(const KParams p) {
   using G = Geo<KV, D>;
   static_assert(G::kTT == kSplitAlign, "flat tiles are the kernel's tiles");
-  __shared__ __attribute__((aligned(16))) uint8_t sm_k[kWaves * G::kKSlotBytes];
-  __shared__ __attribute__((aligned(16))) float sm_sc[kWaves][G::kScales];
+  constexpr int W = G::kFlatWaves;
+  __shared__ __attribute__((aligned(16))) uint8_t sm_k[W * G::kKSlotBytes];
+  __shared__ __attribute__((aligned(16))) float sm_sc[W][G::kScales];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1028,7 +1034,7 @@ paged_decode_flat_kernel(const KParams p) {
   // global wave = j * units + unit: the waves of a workgroup share a range
   // and cover neighbouring kv heads, which read the same pages.
   const int units = p.hkv * p.head_tiles;
-  const int gw = wg * kWaves + wave;
+  const int gw = wg * W + wave;
   if (gw >= units * p.flat_splits) return;  // no barrier follows: waves are independent
   const int unit = gw % units;
   const int j = gw / units;
@@ -1396,7 +1402,7 @@ int build_params(const pa_decode_args *a, bool need_partials, KParams *kp) {
     const int64_t seq_tiles_max = ((int64_t)a->max_blocks * a->block_size + kSplitAlign - 1) / kSplitAlign;
     if ((int64_t)a->batch * seq_tiles_max + a->flat_splits > 0x7fffffff)
       return fail(PA_ERR_UNSUPPORTED, "batch * max tiles per sequence too large for the flat split");
-    if ((int64_t)a->num_kv_heads * head_tiles * a->flat_splits + kWaves > 0x7fffffff)
+    if ((int64_t)a->num_kv_heads * head_tiles * a->flat_splits + kMaxFlatWaves > 0x7fffffff)
       return fail(PA_ERR_UNSUPPORTED, "flat split grid too large");
   }
 
@@ -1450,7 +1456,9 @@ template <int KV, int SC, int D>
 hipError_t launch_decode_t(const KParams &k, int grid, int mode, hipStream_t st) {
   const dim3 g(grid), blk(kWaves * 64);
   if (mode == kFlat) {
-    hipLaunchKernelGGL((paged_decode_flat_kernel<KV, SC, D>), g, blk, 0, st, k);
+    constexpr int W = Geo<KV, D>::kFlatWaves;
+    const int flat_grid = (k.hkv * k.head_tiles * k.flat_splits + W - 1) / W;
+    hipLaunchKernelGGL((paged_decode_flat_kernel<KV, SC, D>), dim3(flat_grid), dim3(W * 64), 0, st, k);
   } else if (mode == kAuto) {
     hipLaunchKernelGGL((paged_decode_kernel<KV, SC, D, kAuto>), g, blk, 0, st, k);
   } else if (mode == kPartials) {
@@ -1472,9 +1480,8 @@ hipError_t launch_decode_d(const KParams &k, int d, int grid, int mode, hipStrea
 }
 
 hipError_t launch_decode(const KParams &k, const pa_decode_args *a, int mode, hipStream_t st) {
-  const int grid = mode == kFlat
-                       ? (a->num_kv_heads * k.head_tiles * a->flat_splits + kWaves - 1) / kWaves
-                       : a->batch * a->num_kv_heads * k.head_tiles * a->num_splits;
+  // the flat launch sizes its own grid from its workgroup width
+  const int grid = mode == kFlat ? 0 : a->batch * a->num_kv_heads * k.head_tiles * a->num_splits;
   const int d = a->head_dim;
   if (a->kv_dtype == PA_KV_FP16) return launch_decode_d<PA_KV_FP16, PA_SCALE_NONE>(k, d, grid, mode, st);
   if (a->kv_dtype == PA_KV_BF16) return launch_decode_d<PA_KV_BF16, PA_SCALE_NONE>(k, d, grid, mode, st);
@@ -1640,19 +1647,32 @@ int pa_flat_merge(const pa_decode_args *a, void *stream) {
   return ok();
 }
 
-int pa_flat_workgroups_per_cu(int kv_dtype, int scale_dtype, int head_dim, int *out) {
+int pa_flat_waves_per_simd(int kv_dtype, int scale_dtype, int head_dim, int *out) {
   if (out == nullptr) return fail(PA_ERR_INVALID, "out is NULL");
   *out = 0;
   if (head_dim != 32 && head_dim != 64 && head_dim != 128 && head_dim != 256)
     return fail(PA_ERR_UNSUPPORTED, "head_dim %d not in (32, 64, 128, 256)", head_dim);
   const void *fn = nullptr;
+  int waves = 0;  // the kernel's workgroup width
   auto pick = [&](auto kv_tag, auto sc_tag) {
     constexpr int KV = decltype(kv_tag)::value, SC = decltype(sc_tag)::value;
     switch (head_dim) {
-      case 32: fn = reinterpret_cast<const void *>(&paged_decode_flat_kernel<KV, SC, 32>); break;
-      case 64: fn = reinterpret_cast<const void *>(&paged_decode_flat_kernel<KV, SC, 64>); break;
-      case 128: fn = reinterpret_cast<const void *>(&paged_decode_flat_kernel<KV, SC, 128>); break;
-      default: fn = reinterpret_cast<const void *>(&paged_decode_flat_kernel<KV, SC, 256>); break;
+      case 32:
+        fn = reinterpret_cast<const void *>(&paged_decode_flat_kernel<KV, SC, 32>);
+        waves = Geo<KV, 32>::kFlatWaves;
+        break;
+      case 64:
+        fn = reinterpret_cast<const void *>(&paged_decode_flat_kernel<KV, SC, 64>);
+        waves = Geo<KV, 64>::kFlatWaves;
+        break;
+      case 128:
+        fn = reinterpret_cast<const void *>(&paged_decode_flat_kernel<KV, SC, 128>);
+        waves = Geo<KV, 128>::kFlatWaves;
+        break;
+      default:
+        fn = reinterpret_cast<const void *>(&paged_decode_flat_kernel<KV, SC, 256>);
+        waves = Geo<KV, 256>::kFlatWaves;
+        break;
     }
   };
   using I = int;
@@ -1670,9 +1690,9 @@ int pa_flat_workgroups_per_cu(int kv_dtype, int scale_dtype, int head_dim, int *
     return fail(PA_ERR_INVALID, "kv_dtype %d / scale_dtype %d is not a supported pair", kv_dtype,
                 scale_dtype);
   int n = 0;
-  const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kWaves * 64, 0);
+  const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, waves * 64, 0);
   if (e != hipSuccess) return fail(PA_ERR_HIP, "occupancy query failed: %s", hipGetErrorString(e));
-  *out = n;
+  *out = n * waves / 4;  // workgroups per CU -> waves per SIMD (4 SIMDs per CU)
   return ok();
 }
 

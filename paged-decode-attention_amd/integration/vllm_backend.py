@@ -45,7 +45,7 @@ from pagedattn.hip_decode import (  # noqa: E402
     MIN_FLAT_TILES_PER_WAVE,
     TILE_TOKENS,
     flat_splits_for,
-    flat_workgroups_per_cu,
+    flat_waves_per_simd,
 )
 from pagedattn.triton_decode import paged_decode_triton, pick_num_splits  # noqa: E402
 
@@ -167,7 +167,7 @@ def decode_forward(impl, layer, query, key, value, kv_cache, attn_metadata, outp
     msl = int(attn_metadata.max_seq_len)
     group = impl.num_heads // impl.num_kv_heads
     flat = flat_splits_for(impl.num_kv_heads, group, _cu_count(query.device),
-                           flat_workgroups_per_cu(cache.kv_dtype, impl.head_size))
+                           flat_waves_per_simd(cache.kv_dtype, impl.head_size))
     if n <= FLAT_MAX_BATCH and n * -(-msl // TILE_TOKENS) >= MIN_FLAT_TILES_PER_WAVE * flat:
         decode(query[:n], cache, out=output[:n], sm_scale=impl.scale, flat_splits=flat)
     else:

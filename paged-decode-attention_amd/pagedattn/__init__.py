@@ -13,7 +13,7 @@ from .cache_ops import reshape_and_cache
 from .hip_decode import (
     decode_partials,
     flat_splits_for,
-    flat_workgroups_per_cu,
+    flat_waves_per_simd,
     paged_decode_hip,
     paged_decode_triton,
     pick_num_splits,
@@ -27,6 +27,6 @@ __all__ = [
     "kv_bytes_per_token",
     "PagedKVCache", "allocate", "quantize_kv", "reshape_and_cache",
     "paged_decode_hip", "paged_decode_triton", "pick_num_splits", "plan_num_splits",
-    "plan_decode", "flat_splits_for", "flat_workgroups_per_cu",
+    "plan_decode", "flat_splits_for", "flat_waves_per_simd",
     "decode_partials", "split_reduce",
 ]

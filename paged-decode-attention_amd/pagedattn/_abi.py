@@ -12,7 +12,7 @@ import os
 import pathlib
 import threading
 
-PA_ABI_VERSION = 3
+PA_ABI_VERSION = 4
 
 PA_OK = 0
 PA_ERR_INVALID = -1
@@ -44,7 +44,7 @@ EXPORTED_SYMBOLS = (
     "pa_split_reduce",
     "pa_cache_write",
     "pa_flat_merge",
-    "pa_flat_workgroups_per_cu",
+    "pa_flat_waves_per_simd",
     "pa_last_error",
     "pa_abi_version",
 )
@@ -186,9 +186,9 @@ def load() -> ctypes.CDLL:
         lib.pa_cache_write.restype = ctypes.c_int
         lib.pa_flat_merge.argtypes = [ctypes.POINTER(PaDecodeArgs), _vp]
         lib.pa_flat_merge.restype = ctypes.c_int
-        lib.pa_flat_workgroups_per_cu.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+        lib.pa_flat_waves_per_simd.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                                   ctypes.POINTER(ctypes.c_int)]
-        lib.pa_flat_workgroups_per_cu.restype = ctypes.c_int
+        lib.pa_flat_waves_per_simd.restype = ctypes.c_int
         lib.pa_last_error.argtypes = []
         lib.pa_last_error.restype = ctypes.c_char_p
         lib.pa_abi_version.argtypes = []

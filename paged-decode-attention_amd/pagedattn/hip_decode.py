@@ -49,11 +49,10 @@ MIN_FLAT_TILES_PER_WAVE = 4
 # loads per lane: above this batch the classic split is used instead (such
 # batches fill the GPU unsplit anyway).
 FLAT_MAX_BATCH = 512
-# Workgroups of the flat kernel per CU when the library cannot be asked (no
-# GPU): register-limited occupancy of the gfx950 build by (bytes per stored
-# element, head_dim).
-_FLAT_WGS_FALLBACK = {(2, 32): 5, (2, 64): 4, (2, 128): 2, (2, 256): 2,
-                      (1, 32): 5, (1, 64): 4, (1, 128): 3, (1, 256): 2}
+# Flat-kernel waves per SIMD when the library cannot be asked (no GPU): the
+# gfx950 build's occupancy by (bytes per stored element, head_dim).
+_FLAT_WAVES_FALLBACK = {(2, 32): 4, (2, 64): 4, (2, 128): 2, (2, 256): 2,
+                        (1, 32): 4, (1, 64): 4, (1, 128): 2, (1, 256): 2}
 
 _KV_CODE = {"fp16": _abi.PA_KV_FP16, "fp8_e5m2": _abi.PA_KV_FP8_E5M2, "int8": _abi.PA_KV_INT8,
             "bf16": _abi.PA_KV_BF16}
@@ -117,18 +116,18 @@ def plan_num_splits(seq_lens, num_kv_heads: int, group: int, sm_count: int) -> t
     return int(splits), tmax
 
 
-def flat_splits_for(num_kv_heads: int, group: int, sm_count: int, workgroups_per_cu: int) -> int:
+def flat_splits_for(num_kv_heads: int, group: int, sm_count: int, waves_per_simd: int) -> int:
     """One round of waves over the (kv head, head tile) units: as many as
-    the CUs hold (4 SIMDs each, `workgroups_per_cu` waves per SIMD), capped at
+    the CUs hold (4 SIMDs each, `waves_per_simd` waves per SIMD), capped at
     FLAT_WAVES_PER_SIMD per SIMD."""
     units = num_kv_heads * -(-group // _abi.PA_MAX_GROUP)
-    per_simd = max(1, min(workgroups_per_cu, FLAT_WAVES_PER_SIMD))
+    per_simd = max(1, min(waves_per_simd, FLAT_WAVES_PER_SIMD))
     waves = max(1, sm_count) * WAVES_PER_WORKGROUP * per_simd
     return int(max(1, min(waves // units, _abi.PA_MAX_FLAT_SPLITS)))
 
 
 def plan_decode(seq_lens, num_kv_heads: int, group: int, sm_count: int,
-                workgroups_per_cu: int = 2) -> tuple[int, int, int]:
+                waves_per_simd: int = 2) -> tuple[int, int, int]:
     """(num_splits, max_seq_len, flat_splits) for a batch whose lengths the host knows.
 
     The flat split (one round of waves, `flat_splits_for`) whenever each of
@@ -139,7 +138,7 @@ def plan_decode(seq_lens, num_kv_heads: int, group: int, sm_count: int,
     """
     lens = [max(0, int(t)) for t in seq_lens]
     tmax = max(lens) if lens else 0
-    flat = flat_splits_for(num_kv_heads, group, sm_count, workgroups_per_cu)
+    flat = flat_splits_for(num_kv_heads, group, sm_count, waves_per_simd)
     tiles = sum(-(-t // TILE_TOKENS) for t in lens)
     if len(lens) <= FLAT_MAX_BATCH and tiles >= MIN_FLAT_TILES_PER_WAVE * flat:
         return 1, tmax, flat
@@ -182,8 +181,8 @@ _CU_COUNT: dict[int, int] = {}
 _FLAT_WGS: dict[tuple, int] = {}
 
 
-def flat_workgroups_per_cu(kv_dtype: str, head_dim: int, scale_dtype: torch.dtype | None = None) -> int:
-    """Resident flat-kernel workgroups per CU, from the library's occupancy
+def flat_waves_per_simd(kv_dtype: str, head_dim: int, scale_dtype: torch.dtype | None = None) -> int:
+    """Resident flat-kernel waves per SIMD, from the library's occupancy
     query on the current device (a built-in table without a GPU)."""
     sc = _abi.PA_SCALE_NONE if kv_dtype != "int8" else _SCALE_CODE.get(scale_dtype or torch.float16)
     key = (kv_dtype, head_dim, sc)
@@ -192,11 +191,11 @@ def flat_workgroups_per_cu(kv_dtype: str, head_dim: int, scale_dtype: torch.dtyp
         n = 0
         if torch.cuda.is_available() and kv_dtype in _KV_CODE:
             got = ctypes.c_int(0)
-            if _abi.load().pa_flat_workgroups_per_cu(_KV_CODE[kv_dtype], sc, head_dim, ctypes.byref(got)) == 0:
+            if _abi.load().pa_flat_waves_per_simd(_KV_CODE[kv_dtype], sc, head_dim, ctypes.byref(got)) == 0:
                 n = got.value
         if n <= 0:
             elem = 2 if kv_dtype in ("fp16", "bf16") else 1
-            n = _FLAT_WGS_FALLBACK.get((elem, head_dim), 2)
+            n = _FLAT_WAVES_FALLBACK.get((elem, head_dim), 2)
         _FLAT_WGS[key] = n
     return n
 
@@ -370,9 +369,9 @@ def paged_decode_hip(
         num_splits = 1
     elif num_splits is None:
         # the lengths come to the host in the one sync the reference also makes
-        wgs = flat_workgroups_per_cu(cache.kv_dtype, d, None if cache.k_scale is None else cache.k_scale.dtype)
+        wps = flat_waves_per_simd(cache.kv_dtype, d, None if cache.k_scale is None else cache.k_scale.dtype)
         num_splits, longest, flat_splits = plan_decode(cache.seq_lens.tolist(), hkv, group,
-                                                       _cu_count(q.device), wgs)
+                                                       _cu_count(q.device), wps)
         if max_seq_len is None:
             max_seq_len = longest
     num_splits = int(num_splits)
@@ -509,7 +508,7 @@ __all__ = [
     "plan_num_splits",
     "plan_decode",
     "flat_splits_for",
-    "flat_workgroups_per_cu",
+    "flat_waves_per_simd",
     "WAVES_PER_WORKGROUP",
     "TILE_TOKENS",
 ]

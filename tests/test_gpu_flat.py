@@ -149,12 +149,12 @@ def test_flat_partial_slots_match_oracle(flat):
 def test_flat_occupancy_query(kv_dtype, scale_dtype, d):
     """The library's occupancy answer sizes flat_splits; the size it gives
     must equal the one the no-GPU fallback table gives."""
-    from pagedattn.hip_decode import _FLAT_WGS_FALLBACK, flat_splits_for, flat_workgroups_per_cu
+    from pagedattn.hip_decode import _FLAT_WAVES_FALLBACK, flat_splits_for, flat_waves_per_simd
 
-    n = flat_workgroups_per_cu(kv_dtype, d, scale_dtype)
+    n = flat_waves_per_simd(kv_dtype, d, scale_dtype)
     print(f"{kv_dtype} d={d}: {n} workgroups/CU")
     assert 1 <= n <= 8
-    table = _FLAT_WGS_FALLBACK[(2 if kv_dtype in ("fp16", "bf16") else 1, d)]
+    table = _FLAT_WAVES_FALLBACK[(2 if kv_dtype in ("fp16", "bf16") else 1, d)]
     assert flat_splits_for(8, 4, 256, n) == flat_splits_for(8, 4, 256, table)
 
 

@@ -365,12 +365,12 @@ def test_flat_splits_for_and_plan_decode():
 def test_flat_occupancy_query_validates_before_hip():
     lib = _lib()
     out = ctypes.c_int(7)
-    assert lib.pa_flat_workgroups_per_cu(_abi.PA_KV_FP16, _abi.PA_SCALE_NONE, 96, ctypes.byref(out)) \
+    assert lib.pa_flat_waves_per_simd(_abi.PA_KV_FP16, _abi.PA_SCALE_NONE, 96, ctypes.byref(out)) \
         == _abi.PA_ERR_UNSUPPORTED
     assert out.value == 0
-    assert lib.pa_flat_workgroups_per_cu(_abi.PA_KV_INT8, _abi.PA_SCALE_NONE, 128, ctypes.byref(out)) \
+    assert lib.pa_flat_waves_per_simd(_abi.PA_KV_INT8, _abi.PA_SCALE_NONE, 128, ctypes.byref(out)) \
         == _abi.PA_ERR_INVALID
-    assert lib.pa_flat_workgroups_per_cu(_abi.PA_KV_FP16, _abi.PA_SCALE_NONE, 128, None) \
+    assert lib.pa_flat_waves_per_simd(_abi.PA_KV_FP16, _abi.PA_SCALE_NONE, 128, None) \
         == _abi.PA_ERR_INVALID
     assert lib.pa_last_error().decode()
 

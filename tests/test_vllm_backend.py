@@ -187,7 +187,7 @@ def test_decode_forward_takes_the_flat_split_for_large_batches(monkeypatch):
     """Host-side routing only: with n * ceil(max_seq_len / 32) tiles enough
     for the flat split's waves, the step launches it (no device sync)."""
     monkeypatch.setattr(vb, "_cu_count", lambda dev: 256)
-    monkeypatch.setattr(vb, "flat_workgroups_per_cu", lambda kv, d: 2)
+    monkeypatch.setattr(vb, "flat_waves_per_simd", lambda kv, d: 2)
     calls = []
 
     def fake_decode(q, cache, out, sm_scale, **kw):
