@@ -2,16 +2,20 @@
 //
 // Replaces the two Triton kernels of the reference
 // (ParamThakkar123/paged-decode-attention, pagedattn/triton_decode.py):
-//   _paged_decode_kernel  (:33-195)  -> paged_decode_kernel<...>
+//   _paged_decode_kernel  (:33-195)  -> paged_decode_kernel<...> (unsplit and
+//                                       the reference's per-sequence split)
+//                                       and paged_decode_flat_kernel<...> (a
+//                                       work-balanced split, no counterpart)
 //   _split_reduce_kernel  (:198-240) -> split_reduce_kernel
 // and the launch section of `paged_decode_triton` (:331-376) -> pa_decode.
 //
-// Work decomposition. One workgroup of kWaves wave64s per
-// (batch, kv_head, head_tile, split). The workgroup's token range [lo, hi) is
-// cut into 32-token tiles; wave w takes tiles w, w + kWaves, ... Every wave
-// keeps its own online-softmax state in VGPRs and the waves are merged once
-// through LDS at the end, so a workgroup is a split of kWaves sub-splits that
-// costs a single partial write.
+// Work decomposition (paged_decode_kernel). One workgroup of kWaves wave64s
+// per (batch, kv_head, head_tile, split). The workgroup's token range
+// [lo, hi) is cut into 32-token tiles; wave w takes tiles w, w + kWaves, ...
+// Every wave keeps its own online-softmax state in VGPRs and the waves are
+// merged once through LDS at the end, so a workgroup is a split of kWaves
+// sub-splits that costs a single partial write. The flat kernel's
+// decomposition is described at its definition.
 //
 // Each wave double-buffers its tiles in registers: the K/V loads of its next
 // tile are issued before the current tile is computed, so HBM requests stay in
@@ -25,8 +29,9 @@
 //   O^T[d, h] += V^T[d, tok] P^T[tok, h] v_mfma_f32_16x16x32_f16, A = V^T,
 //                                        B = P^T taken straight from the QK
 //                                        accumulator layout (no shuffles)
-// K rows are loaded in 16-byte pieces directly into the MFMA A-operand layout.
-// V rows are loaded in the natural [tok][d] layout, 16 lanes covering one row
+// K rows are loaded whole (consecutive lanes, consecutive 16-byte pieces) into
+// a per-wave LDS slot and read back in the MFMA A-operand layout. V rows are
+// loaded in the natural [tok][d] layout, 16 lanes covering one row
 // contiguously, and transposed to [d][tok] pairs in registers with v_perm.
 // All `group` query heads of a kv head share the tile (padded to the 16 MFMA
 // columns), so each K/V byte is read from HBM once.
@@ -196,8 +201,8 @@ __device__ __forceinline__ constexpr uint32_t pair_sel(uint32_t i, uint32_t j) {
   }
 }
 
-// Two stored bytes -> two fp16 bit patterns: one v_perm (int8 words arrive
-// with the sign bits already flipped).
+// Two stored bytes -> two fp16 bit patterns: one v_perm (int8 sign bits are
+// flipped on the K words before it and on the V pair after it).
 template <int KV>
 __device__ __forceinline__ uint32_t bytes_to_halves(uint32_t hi, uint32_t lo, uint32_t sel) {
   return perm(hi, lo, sel);
@@ -917,7 +922,7 @@ paged_decode_kernel(const KParams p) {
 // normalised output and log2-sum-exp as partial slot b + j (j = the wave's
 // range index), or `out` itself when the segment is the whole sequence.
 // Slots are unique: if range j - 1 reached sequence b + 1, sequence b ended
-// before range j began. The merge (split_reduce_kernel<D, kFlatMerge>)
+// before range j began. The merge (split_reduce_kernel<D, kMergeFlat>)
 // derives the same ranges from seq_lens and folds slots b + j0 .. b + j1.
 // ----------------------------------------------------------------------------
 
