@@ -187,3 +187,34 @@ def test_flat_batches_above_one_wave(batch, flat):
     shape = ModelShape(8, 2, 64, "b")
     q, c = _case(shape, lens, seed=10)
     _check(q, c, flat)
+
+
+def test_flat_sm_scale_override():
+    q, c = _case(LLAMA3_8B, [300, 7, 900], seed=11)
+    got = paged_decode_hip(q, c, sm_scale=0.05, flat_splits=13)
+    torch.cuda.synchronize()
+    want = oracle.reference_decode(q, c, sm_scale=0.05, out_dtype=torch.float32)
+    assert max_abs(got, want) < ABS_TOL
+
+
+def test_flat_vllm_style_strided_views():
+    """K/V as `kv_cache.unbind(0)` views, q/out as slices of larger buffers."""
+    c = allocate(LLAMA3_8B, 3, [100, 1, 513], seed=12, device="cuda")
+    kv = torch.stack([c.k_cache, c.v_cache])
+    c.k_cache, c.v_cache = kv.unbind(0)
+    qbuf = seeded_q(5, 32, 128, 12, device="cuda")
+    outbuf = torch.zeros((5, 32, 128), dtype=torch.float16, device="cuda")
+    paged_decode_hip(qbuf[:3], c, out=outbuf[:3], flat_splits=9)
+    torch.cuda.synchronize()
+    want = oracle.reference_decode(qbuf[:3], c, out_dtype=torch.float32)
+    assert max_abs(outbuf[:3], want) < ABS_TOL
+    assert torch.equal(outbuf[3:], torch.zeros_like(outbuf[3:])), "wrote outside out"
+
+
+def test_flat_merge_of_many_slots():
+    """A sequence cut into more slots than the merge holds in registers (32)
+    and than it stages in LDS at once (256)."""
+    lens = [40000, 3, 700]
+    q, c = _case(LLAMA3_8B, lens, seed=13)
+    _check(q, c, 1000)   # per = 2 tiles: the long sequence spans 625 slots
+    _check(q, c, 40)     # per = 33 tiles: 38 slots
