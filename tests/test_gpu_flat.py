@@ -218,3 +218,32 @@ def test_flat_merge_of_many_slots():
     q, c = _case(LLAMA3_8B, lens, seed=13)
     _check(q, c, 1000)   # per = 2 tiles: the long sequence spans 625 slots
     _check(q, c, 40)     # per = 33 tiles: 38 slots
+
+
+@pytest.mark.parametrize("kw", [{"flat_splits": 29}, {"num_splits": 5, "max_seq_len": 4096},
+                                {"num_splits": 1}])
+def test_decode_in_a_hip_graph(kw):
+    """A fixed-shape decode captured in a HIP graph (no allocation, sync or
+    memset inside a launch) replays correctly: three replays with new q
+    values, eager work and synchronisations in between, each equal to the
+    eager result bit for bit."""
+    q, c = _case(LLAMA3_8B, RAGGED, seed=14)
+    out = torch.empty_like(q)
+    paged_decode_hip(q, c, out=out, **kw)  # workspace allocated outside the capture
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        paged_decode_hip(q, c, out=out, **kw)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        paged_decode_hip(q, c, out=out, **kw)
+    for seed in (15, 16, 17):
+        q.copy_(seeded_q(q.shape[0], 32, 128, seed, device="cuda"))
+        eager = paged_decode_hip(q, c, **kw).clone()
+        torch.cuda.synchronize()
+        out.fill_(7.0)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay with q seed {seed} differs"
