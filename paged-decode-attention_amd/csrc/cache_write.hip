@@ -107,12 +107,21 @@ __global__ void __launch_bounds__(256) cache_write_kernel(const WParams p) {
       // IEEE division (the default for float `/` in HIP device code)
       float scale = amax / 127.0f;
       if constexpr (SC == PA_SCALE_FP16) scale = (float)(_Float16)scale;
+      // round_half_even(x / scale) with the IEEE quotient's rounding: x times
+      // the row's reciprocal is within 1.5 ulp of the correctly rounded
+      // quotient, so the two can round to different integers only next to a
+      // half-integer; those (rare) elements take the IEEE division
+      const float inv = 1.0f / scale;
       uint32_t b[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
+        const float q0 = x[i] * inv;
+        const float frac = q0 - floorf(q0);
+        const float tol = fabsf(q0) * 0x1p-20f + 0x1p-40f;
+        float r = rintf(q0);
+        if (fabsf(frac - 0.5f) <= tol) r = rintf(x[i] / scale);
         // a zero row with fp16 scales underflows the scale to 0: 0/0 is NaN,
         // which the reference's cast to int8 stores as 0
-        const float r = rintf(x[i] / scale);
         const float q = (r != r) ? 0.f : fminf(fmaxf(r, -127.f), 127.f);
         b[i] = (uint32_t)(int32_t)q & 0xffu;
       }

@@ -124,3 +124,34 @@ def test_bf16_rows_into_bf16_cache():
     oracle.write_kv(key, value, ref, slots)
     torch.cuda.synchronize()
     assert torch.equal(c.k_cache.cpu(), ref.k_cache) and torch.equal(c.v_cache.cpu(), ref.v_cache)
+
+
+@pytest.mark.parametrize("scale_dtype", [torch.float16, torch.float32])
+def test_int8_quotients_on_and_next_to_half_integers(scale_dtype):
+    """Rows whose x / scale land exactly on half-integers (ties to even) and
+    one fp16 step away from them: the writer's rounding equals torch's IEEE
+    division + round-half-even there too."""
+    shape = ModelShape(2, 1, 128, "h")
+    c = allocate(shape, 1, [256], kv_dtype="int8", scale_dtype=scale_dtype, seed=48, device="cuda",
+                 shuffle=False)
+    ref = _cpu_copy(c)
+    rows = []
+    for amax in (127.0, 254.0, 100.0, 3.0, 1000.0):
+        scale = torch.tensor(amax / 127.0, dtype=torch.float32).to(scale_dtype).float().item()
+        k = torch.arange(-63, 64, dtype=torch.float32)          # 127 half-integers
+        xs = ((k + 0.5) * scale).half()
+        for step in (0, 1, -1):                                  # on, and one fp16 step off
+            v = xs.view(torch.int16) + step
+            v = torch.where(xs == 0, xs.view(torch.int16), v)
+            row = torch.cat([v.view(torch.float16), torch.tensor([amax], dtype=torch.float16)])
+            rows.append(row)
+    key = torch.stack(rows).view(-1, 1, 128)
+    value = key.flip(0).contiguous()
+    n = key.shape[0]
+    slots = torch.arange(n, dtype=torch.int64)
+    reshape_and_cache(key.cuda(), value.cuda(), c, slots.cuda())
+    oracle.write_kv(key, value, ref, slots)
+    torch.cuda.synchronize()
+    assert torch.equal(_raw(c.k_cache.cpu()), _raw(ref.k_cache))
+    assert torch.equal(_raw(c.v_cache.cpu()), _raw(ref.v_cache))
+    assert torch.equal(c.k_scale.cpu(), ref.k_scale) and torch.equal(c.v_scale.cpu(), ref.v_scale)
