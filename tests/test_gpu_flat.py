@@ -247,3 +247,29 @@ def test_decode_in_a_hip_graph(kw):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay with q seed {seed} differs"
+
+
+@pytest.mark.parametrize("kw", [{"flat_splits": 7}, {"num_splits": 3}, {"num_splits": 1}])
+def test_out_of_range_lengths_and_block_ids_are_clamped(kw):
+    """The kernels' own bounds: a length past the block table reads the whole
+    table, a negative length is empty, block ids outside the pool are clamped
+    into it. Equal to the oracle on the clamped inputs."""
+    import dataclasses
+
+    c = allocate(LLAMA3_8B, 4, [70, 128, 40, 16], seed=15, device="cuda", slack_blocks=3)
+    nb = c.k_cache.shape[0]
+    bt = c.block_table.clone()
+    assert bt.shape[1] == 8
+    bt[2, 1] = nb + 5      # inside sequence 2 (40 tokens): clamped to nb - 1
+    bt[3, 0] = -3          # inside sequence 3: clamped to 0
+    lens = torch.tensor([70, 10**6, 40, -5], dtype=torch.int32, device="cuda")
+    bad = dataclasses.replace(c, block_table=bt, seq_lens=lens)
+    q = seeded_q(4, 32, 128, 15, device="cuda")
+    got = paged_decode_hip(q, bad, **kw)
+    torch.cuda.synchronize()
+    good_bt = bt.clamp(0, nb - 1)
+    good = dataclasses.replace(c, block_table=good_bt,
+                               seq_lens=torch.tensor([70, 8 * 16, 40, 0], dtype=torch.int32, device="cuda"))
+    want = oracle.reference_decode(q, good, out_dtype=torch.float32)
+    assert max_abs(got[:3], want[:3]) < ABS_TOL
+    assert torch.equal(got[3].cpu(), torch.zeros_like(got[3].cpu()))
