@@ -226,92 +226,100 @@ def _fill_args(
 ) -> _abi.PaDecodeArgs:
     b, hq, d = q.shape
     shape = cache.shape
-    if cache.kv_dtype not in _KV_CODE:
-        raise NotImplementedError(f"kv_dtype {cache.kv_dtype!r} is not supported by the HIP kernel")
+    kv_dtype = cache.kv_dtype
+    if kv_dtype not in _KV_CODE:
+        raise NotImplementedError(f"kv_dtype {kv_dtype!r} is not supported by the HIP kernel")
     if q.dtype not in _IO_CODE or out.dtype != q.dtype:
         raise NotImplementedError(f"q/out dtype {q.dtype}/{out.dtype}: float16 or bfloat16, the same for both")
-    if q.device.type != "cuda":
+    if not q.is_cuda:
         raise ValueError(f"q is on {q.device}: the HIP decode kernel needs GPU tensors")
     k, v = cache.k_cache, cache.v_cache
-    for name, t in (("k_cache", k), ("v_cache", v), ("out", out),
-                    ("block_table", cache.block_table), ("seq_lens", cache.seq_lens)):
-        if t.device != q.device:
+    bt, sl = cache.block_table, cache.seq_lens
+    dev = q.get_device()
+    for name, t in (("k_cache", k), ("v_cache", v), ("out", out), ("block_table", bt), ("seq_lens", sl)):
+        if t.get_device() != dev:
             raise ValueError(f"{name} is on {t.device}, q on {q.device}")
-    if k.dtype != _STORE_DTYPE[cache.kv_dtype] or v.dtype != k.dtype:
-        raise ValueError(f"k/v cache dtype {k.dtype}/{v.dtype} does not match kv_dtype {cache.kv_dtype}")
-    if k.dim() != 4 or tuple(k.shape[1:]) != (cache.block_size, shape.num_kv_heads, d):
-        raise ValueError(f"k_cache shape {tuple(k.shape)} is not [NB, {cache.block_size}, "
+    if k.dtype != _STORE_DTYPE[kv_dtype] or v.dtype != k.dtype:
+        raise ValueError(f"k/v cache dtype {k.dtype}/{v.dtype} does not match kv_dtype {kv_dtype}")
+    kshape, kst = k.shape, k.stride()
+    if len(kshape) != 4 or tuple(kshape[1:]) != (cache.block_size, shape.num_kv_heads, d):
+        raise ValueError(f"k_cache shape {tuple(kshape)} is not [NB, {cache.block_size}, "
                          f"{shape.num_kv_heads}, {d}]")
-    if tuple(v.shape) != tuple(k.shape) or v.stride() != k.stride():
+    if v.shape != kshape or v.stride() != kst:
         raise ValueError("v_cache must have k_cache's shape and strides")
-    if k.stride(3) != 1 or q.stride(2) != 1 or out.stride(2) != 1:
+    qst, ost = q.stride(), out.stride()
+    if kst[3] != 1 or qst[2] != 1 or ost[2] != 1:
         raise ValueError("head_dim must be the contiguous (stride-1) dimension of q, out and the caches")
     if tuple(out.shape) != (b, hq, d):
         raise ValueError(f"out shape {tuple(out.shape)} != {(b, hq, d)}")
-    bt, sl = cache.block_table, cache.seq_lens
     if bt.dtype != torch.int32 or sl.dtype != torch.int32:
         raise ValueError("block_table and seq_lens must be int32")
-    if bt.dim() != 2 or bt.shape[0] != b or sl.shape != (b,):
-        raise ValueError(f"block_table {tuple(bt.shape)} / seq_lens {tuple(sl.shape)} do not match batch {b}")
-    if bt.stride(1) != 1 or sl.stride(0) != 1:
+    btshape, btst = bt.shape, bt.stride()
+    if len(btshape) != 2 or btshape[0] != b or tuple(sl.shape) != (b,):
+        raise ValueError(f"block_table {tuple(btshape)} / seq_lens {tuple(sl.shape)} do not match batch {b}")
+    if btst[1] != 1 or sl.stride(0) != 1:
         raise ValueError("block_table rows and seq_lens must be contiguous")
 
-    a = _abi.PaDecodeArgs()
-    a.q = q.data_ptr()
-    a.k_cache = k.data_ptr()
-    a.v_cache = v.data_ptr()
-    a.out = out.data_ptr()
-    a.block_table = bt.data_ptr()
-    a.seq_lens = sl.data_ptr()
-    a.batch = b
-    a.num_q_heads = hq
-    a.num_kv_heads = shape.num_kv_heads
-    a.head_dim = d
-    a.block_size = cache.block_size
-    a.num_blocks = k.shape[0]
-    a.max_blocks = bt.shape[1]
-    a.num_splits = num_splits
-    a.max_seq_len = int(max_seq_len)
-    a.stride_qb, a.stride_qh = q.stride(0), q.stride(1)
-    a.stride_kn, a.stride_kt, a.stride_kh = k.stride(0), k.stride(1), k.stride(2)
-    a.stride_ob, a.stride_oh = out.stride(0), out.stride(1)
-    a.stride_btb = bt.stride(0)
-    a.kv_dtype = _KV_CODE[cache.kv_dtype]
-    a.io_dtype = _IO_CODE[q.dtype]
-    a.sm_scale = sm_scale
-    if cache.kv_dtype == "int8":
+    k_scale = v_scale = None
+    sst = (0, 0)
+    scale_code = _abi.PA_SCALE_NONE
+    if kv_dtype == "int8":
         ks, vs = cache.k_scale, cache.v_scale
         if ks is None or vs is None:
             raise ValueError("int8 cache needs k_scale and v_scale")
         if ks.dtype not in _SCALE_CODE or vs.dtype != ks.dtype:
             raise ValueError(f"int8 scales must be float16 or float32, got {ks.dtype}/{vs.dtype}")
-        if tuple(ks.shape) != tuple(k.shape[:3]) or vs.stride() != ks.stride() or ks.stride(2) != 1:
+        sst = ks.stride()
+        if tuple(ks.shape) != tuple(kshape[:3]) or vs.stride() != sst or sst[2] != 1:
             raise ValueError("k_scale/v_scale must be [NB, block_size, H_kv] with equal strides "
                              "and a contiguous head dimension")
-        if ks.device != q.device or vs.device != q.device:
+        if ks.get_device() != dev or vs.get_device() != dev:
             raise ValueError("scales must live on q's device")
-        a.k_scale = ks.data_ptr()
-        a.v_scale = vs.data_ptr()
-        a.stride_sn, a.stride_st = ks.stride(0), ks.stride(1)
-        a.scale_dtype = _SCALE_CODE[ks.dtype]
-    else:
-        a.scale_dtype = _abi.PA_SCALE_NONE
-    a.flat_splits = int(flat_splits)
+        k_scale, v_scale = ks.data_ptr(), vs.data_ptr()
+        scale_code = _SCALE_CODE[ks.dtype]
+
+    po = pl = None
+    pst = (0, 0, 0)
+    lst = (0, 0)
     if part_out is not None:
-        a.part_out = part_out.data_ptr()
-        a.part_lse = part_lse.data_ptr()
+        po, pl = part_out.data_ptr(), part_lse.data_ptr()
         if flat_splits > 0:  # slots [B + F, Hq, D] / [B + F, Hq]
             if part_out.dim() != 3 or part_out.shape[0] < b + flat_splits or part_lse.shape[0] < b + flat_splits:
                 raise ValueError(f"flat split workspace needs {b + flat_splits} slots")
-            a.stride_pb, a.stride_ph, a.stride_ps = part_out.stride(0), part_out.stride(1), 0
+            pst = (part_out.stride(0), part_out.stride(1), 0)
         else:
-            a.stride_pb, a.stride_ph, a.stride_ps = part_out.stride(0), part_out.stride(1), part_out.stride(2)
-        a.stride_lb, a.stride_lh = part_lse.stride(0), part_lse.stride(1)
-    return a
+            pst = part_out.stride()[:3]
+        lst = part_lse.stride()[:2]
+
+    # one constructor call, fields in declaration order (include/pagedattn.h)
+    return _abi.PaDecodeArgs(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), k_scale, v_scale, out.data_ptr(), po, pl,
+        bt.data_ptr(), sl.data_ptr(),
+        b, hq, shape.num_kv_heads, d, cache.block_size, kshape[0], btshape[1], num_splits,
+        int(max_seq_len),
+        qst[0], qst[1], kst[0], kst[1], kst[2], sst[0], sst[1], ost[0], ost[1],
+        pst[0], pst[1], pst[2], lst[0], lst[1], btst[0],
+        _KV_CODE[kv_dtype], scale_code, _IO_CODE[q.dtype], sm_scale, int(flat_splits))
+
+
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
 def _stream(device: torch.device) -> int:
+    """Handle of torch's current stream on `device` (the raw handle when torch
+    exposes it: a Stream object per call costs more than the launch)."""
+    if _raw_stream is not None:
+        return _raw_stream(device.index if device.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def _call(device: torch.device, fn, *args) -> int:
+    """fn(*args) with `device` current (switching only when it is not)."""
+    idx = device.index
+    if idx is None or idx == torch.cuda.current_device():
+        return fn(*args)
+    with torch.cuda.device(device):
+        return fn(*args)
 
 
 def paged_decode_hip(
@@ -386,8 +394,7 @@ def paged_decode_hip(
         part_out, part_lse = _WS.get(b, hq, num_splits, d, q.device)
     args = _fill_args(q, cache, out, num_splits, scale, part_out, part_lse, max_seq_len or 0, flat)
     lib = _abi.load()
-    with torch.cuda.device(q.device):
-        rc = lib.pa_decode(ctypes.byref(args), _stream(q.device))
+    rc = _call(q.device, lib.pa_decode, ctypes.byref(args), _stream(q.device))
     _abi.check(rc, "pa_decode")
     return out
 
@@ -433,8 +440,7 @@ def decode_partials(
         out = torch.empty((b, hq, d), dtype=q.dtype, device=q.device)
     args = _fill_args(q, cache, out, num_splits, scale, part_out, part_lse, max_seq_len, flat_splits)
     lib = _abi.load()
-    with torch.cuda.device(q.device):
-        rc = lib.pa_decode_partials(ctypes.byref(args), _stream(q.device))
+    rc = _call(q.device, lib.pa_decode_partials, ctypes.byref(args), _stream(q.device))
     _abi.check(rc, "pa_decode_partials")
     return part_out, part_lse
 
@@ -456,8 +462,7 @@ def flat_merge(
     scale = cache.shape.softmax_scale if sm_scale is None else float(sm_scale)
     args = _fill_args(q, cache, out, 1, scale, part_out, part_lse, 0, flat_splits)
     lib = _abi.load()
-    with torch.cuda.device(q.device):
-        rc = lib.pa_flat_merge(ctypes.byref(args), _stream(q.device))
+    rc = _call(q.device, lib.pa_flat_merge, ctypes.byref(args), _stream(q.device))
     _abi.check(rc, "pa_flat_merge")
     return out
 
@@ -485,8 +490,7 @@ def split_reduce(
     r.stride_ob, r.stride_oh = out.stride(0), out.stride(1)
     r.io_dtype = _IO_CODE[out.dtype]
     lib = _abi.load()
-    with torch.cuda.device(part_out.device):
-        rc = lib.pa_split_reduce(ctypes.byref(r), _stream(part_out.device))
+    rc = _call(part_out.device, lib.pa_split_reduce, ctypes.byref(r), _stream(part_out.device))
     _abi.check(rc, "pa_split_reduce")
     return out
 
