@@ -298,29 +298,78 @@ def test_flat_segments_known_answer():
     assert oracle.flat_segments([0, 0], 4) == ([], 1)
 
 
-@pytest.mark.parametrize("flat_splits", [1, 2, 5, 13, 64, 500])
-def test_flat_segments_partition(flat_splits):
-    g = torch.Generator().manual_seed(21)
-    lens = torch.randint(0, 3000, (37,), generator=g).tolist()
-    lens[3] = 0
-    lens[10] = 1
-    segs, per = oracle.flat_segments(lens, flat_splits)
+def _flat_partition_errors(lens, flat_splits, segs, per):
+    """Violations of the flat split's contract by a work list (empty if none)."""
+    errs = []
     # every sequence is covered exactly once, in order, by tile-aligned pieces
     for b, t in enumerate(lens):
-        mine = [(lo, hi) for _, bb, lo, hi in segs if bb == b]
         pos = 0
-        for lo, hi in mine:
-            assert lo == pos and lo % 32 == 0 and hi > lo
+        for _, bb, lo, hi in segs:
+            if bb != b:
+                continue
+            if lo != pos or lo % 32 or hi <= lo:
+                errs.append(f"sequence {b}: piece [{lo}, {hi}) after {pos}")
             pos = hi
-        assert pos == t
-    # a range holds at most `per` tiles, ranges are in order, slots are unique
+        if pos != t:
+            errs.append(f"sequence {b}: covered to {pos} of {t}")
+    # a range holds at most `per` tiles, all ranges exist, they are in order,
+    # and the slots b + j are unique
     tiles = {}
     for j, _, lo, hi in segs:
         tiles[j] = tiles.get(j, 0) + -(-(hi - lo) // 32)
-    assert max(tiles.values()) <= per and max(tiles) < flat_splits
-    assert [j for j, *_ in segs] == sorted(j for j, *_ in segs)
+    if tiles and (max(tiles.values()) > per or max(tiles) >= flat_splits):
+        errs.append("a range is over-full or out of bounds")
+    if [j for j, *_ in segs] != sorted(j for j, *_ in segs):
+        errs.append("ranges out of order")
     slots = [b + j for j, b, _, _ in segs]
-    assert len(set(slots)) == len(slots)
+    if len(set(slots)) != len(slots):
+        errs.append("slot collision")
+    return errs
+
+
+def _ragged_lens(seed=21, n=37):
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(0, 3000, (n,), generator=g).tolist()
+    lens[3] = 0
+    lens[10] = 1
+    return lens
+
+
+@pytest.mark.parametrize("flat_splits", [1, 2, 5, 13, 64, 500])
+def test_flat_segments_partition(flat_splits):
+    lens = _ragged_lens()
+    segs, per = oracle.flat_segments(lens, flat_splits)
+    assert _flat_partition_errors(lens, flat_splits, segs, per) == []
+
+
+@pytest.mark.parametrize("mistake", ["floor_per", "tile_end_past_length", "unaligned_start",
+                                     "dropped_empty_skip"])
+def test_planted_flat_mistakes_are_caught(mistake):
+    """Mutated restatements of the flat work list fail the partition check."""
+    lens = _ragged_lens()
+    flat_splits = 13
+
+    def mutated(seq_lens, f, align=32):
+        tiles = [-(-max(0, t) // align) for t in seq_lens]
+        total = sum(tiles)
+        per = max(1, total // f) if mistake == "floor_per" else max(1, -(-total // f))
+        segs, cu = [], 0
+        for b, (t, n) in enumerate(zip(seq_lens, tiles)):
+            if mistake == "dropped_empty_skip" and n == 0:
+                segs.append((cu // per, b, 0, 0))
+            fpos = cu
+            while fpos < cu + n:
+                j = fpos // per
+                end = min(cu + n, (j + 1) * per)
+                lo = (fpos - cu) * align + (1 if mistake == "unaligned_start" and fpos > cu else 0)
+                hi = (end - cu) * align if mistake == "tile_end_past_length" else min((end - cu) * align, t)
+                segs.append((j, b, lo, hi))
+                fpos = end
+            cu += n
+        return segs, per
+
+    segs, per = mutated(lens, flat_splits)
+    assert _flat_partition_errors(lens, flat_splits, segs, per), f"{mistake} not caught"
 
 
 @pytest.mark.parametrize("flat_splits", [1, 3, 8, 40])
