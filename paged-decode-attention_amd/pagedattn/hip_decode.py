@@ -7,11 +7,11 @@ and `pick_num_splits` (:248-263); the launch itself goes through the C ABI of
 if the library is missing or the tensors are not on a GPU, the call raises.
 
 Knobs of the reference that only steer Triton code generation (`per_page_bt`,
-`num_warps`, `num_stages`) are accepted and ignored: the HIP kernel always
-reads one block-table entry per 16-token sub-tile (one per page at page size
-16) and has a fixed 4-wave workgroup. `block_n` keeps the reference's check
-that it is a multiple of the page size; split ranges are aligned to the
-kernel's 32-token tile.
+`num_warps`, `num_stages`) are accepted and ignored: the HIP kernels always
+read one block-table entry per 16-token sub-tile (one per page at page size
+16) and size their workgroups themselves (4 waves; the flat kernel 4 or 8 by
+row width). `block_n` keeps the reference's check that it is a multiple of
+the page size; split ranges are aligned to the kernels' 32-token tile.
 """
 
 from __future__ import annotations
@@ -25,9 +25,10 @@ from . import _abi
 from .cache import PagedKVCache
 
 # Work geometry of the decode kernel (csrc/paged_decode.hip): 4 wave64s per
-# workgroup, 32 tokens per wave iteration.
+# workgroup, 32 tokens per wave iteration; a CU has 4 SIMDs.
 WAVES_PER_WORKGROUP = 4
 TILE_TOKENS = 32
+SIMDS_PER_CU = 4
 # Workgroups of the decode kernel resident on one CU at head_dim 128 (two
 # 4-wave workgroups: the kernel is built for 2 waves per SIMD).
 RESIDENT_WORKGROUPS_PER_CU = 2
@@ -122,7 +123,7 @@ def flat_splits_for(num_kv_heads: int, group: int, sm_count: int, waves_per_simd
     FLAT_WAVES_PER_SIMD per SIMD."""
     units = num_kv_heads * -(-group // _abi.PA_MAX_GROUP)
     per_simd = max(1, min(waves_per_simd, FLAT_WAVES_PER_SIMD))
-    waves = max(1, sm_count) * WAVES_PER_WORKGROUP * per_simd
+    waves = max(1, sm_count) * SIMDS_PER_CU * per_simd
     return int(max(1, min(waves // units, _abi.PA_MAX_FLAT_SPLITS)))
 
 
@@ -132,9 +133,9 @@ def plan_decode(seq_lens, num_kv_heads: int, group: int, sm_count: int,
 
     The flat split (one round of waves, `flat_splits_for`) whenever each of
     its waves gets at least MIN_FLAT_TILES_PER_WAVE tiles and the batch is at
-    most FLAT_MAX_BATCH: it is
-    balanced for any mix of lengths and measured fastest on every BASELINE
-    split shape. Smaller batches take `plan_num_splits`.
+    most FLAT_MAX_BATCH: it is balanced for any mix of lengths and measured
+    fastest on every BASELINE split shape. Smaller batches take
+    `plan_num_splits`.
     """
     lens = [max(0, int(t)) for t in seq_lens]
     tmax = max(lens) if lens else 0
