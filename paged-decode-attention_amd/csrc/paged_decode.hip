@@ -287,10 +287,9 @@ struct Geo {
   // largest instance that measured best double-buffered: fp16 at D = 128)
   static constexpr int kTileWords = 4 * kKLoads + kVRows * kVWords;
   static constexpr bool kPrefetch = 2 * kTileWords + 4 * kE + 4 * kKSteps <= 176;
-  // Flat-kernel workgroup: one wave per neighbouring kv head, enough of them
-  // that a workgroup reads about 1 KB of every token row of a page at once
-  // (4 heads of 256-B rows, 8 of 128-B rows), the width measured fastest.
-  static constexpr int kFlatWaves = kRowBytes <= 128 ? 8 : 4;
+  // Flat-kernel workgroup: one wave per SIMD of a CU, on 4 neighbouring kv
+  // heads (the flat split launches one such workgroup per CU).
+  static constexpr int kFlatWaves = 4;
 };
 
 // Registers of one tile of one wave.
@@ -952,7 +951,6 @@ __device__ __forceinline__ int wave_incl_scan(int x, int lane) {
 __device__ __forceinline__ int flat_total(const ro_i32 *seq_lens, int batch, int max_tokens,
                                           int lane, int &len0) {
   int total = 0;
-#pragma unroll 4
   for (int base = 0; base < batch; base += 64) {
     const int b = base + lane;
     const int len = b < batch ? max(0, min(seq_lens[b], max_tokens)) : 0;
@@ -1012,9 +1010,11 @@ __device__ __forceinline__ void cursor_next(SeqCursor &cur, const ro_i32 *seq_le
   }
 }
 
-// Built for two waves per SIMD, the count the flat split launches (more
-// streaming waves measured slower); 1-byte KV at head_dim 128 would fit
-// three, and the looser register budget measured marginally faster.
+// The flat split launches one wave per SIMD. With two, a SIMD's older wave
+// runs ahead of the younger one (per-wave timestamps: the younger finish up
+// to 20% later), and that tail costs more than the second wave brings. The
+// register budget is still that of two waves per SIMD, the budget every
+// instance was tuned under.
 template <int KV, int SC, int D>
 __global__ void __launch_bounds__((Geo<KV, D>::kFlatWaves * 64)) __attribute__((amdgpu_waves_per_eu(2)))
 paged_decode_flat_kernel(const KParams p) {
@@ -1193,7 +1193,6 @@ __global__ void __launch_bounds__(kMergeWaves * 64) split_reduce_kernel(const RP
   } else if (KIND == kMergeFlat) {
     // the decode's ranges: per = ceil(total / F) flat tiles each
     int total = 0, cu = 0;
-#pragma unroll 4
     for (int base = 0; base < p.batch; base += 64) {
       const int bb = base + lane;
       const int t = bb < p.batch ? seq_tiles(ro(p.seq_lens), bb, p.max_tokens) : 0;

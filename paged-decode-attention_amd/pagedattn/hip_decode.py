@@ -39,12 +39,13 @@ MIN_SPLIT_TOKENS = 512
 SPLIT_ROUNDS = 2
 
 # Flat split: one round of waves, at most FLAT_WAVES_PER_SIMD per SIMD even
-# where the registers allow more (1-byte KV fits 3): two streaming waves per
-# SIMD measured fastest on every BASELINE split shape (C4 171 us at 2, 183 at
-# 3; a second round or an uneven 2.5 per SIMD is slower still). Used when
-# each wave gets at least MIN_FLAT_TILES_PER_WAVE 32-token tiles; smaller
-# batches are latency-bound and run faster unsplit.
-FLAT_WAVES_PER_SIMD = 2
+# where the registers allow more. One streaming wave per SIMD measured
+# fastest on every BASELINE split shape: with two, each SIMD's older wave
+# runs ahead and the younger ones form a tail (C2 158.5 us at 1, 159.6 at 2;
+# C3 39.3 and 40.6; C5 312.7 and 316.5; three per SIMD or a second round is
+# slower still). Used when each wave gets at least MIN_FLAT_TILES_PER_WAVE
+# 32-token tiles; smaller batches are latency-bound and run faster unsplit.
+FLAT_WAVES_PER_SIMD = 1
 MIN_FLAT_TILES_PER_WAVE = 4
 # Every flat wave (and every merge wave) scans seq_lens once, batch / 64
 # loads per lane: above this batch the classic split is used instead (such

@@ -335,16 +335,17 @@ def test_plan_num_splits():
 def test_flat_splits_for_and_plan_decode():
     from pagedattn import flat_splits_for, plan_decode
 
-    # one round of waves over the (kv head, head tile) units, at most two per SIMD
-    assert flat_splits_for(8, 4, 256, 2) == 256
-    assert flat_splits_for(8, 4, 256, 3) == 256
+    # one round of waves over the (kv head, head tile) units, one per SIMD
+    # whatever the occupancy allows
+    assert flat_splits_for(8, 4, 256, 2) == 128
+    assert flat_splits_for(8, 4, 256, 3) == 128
     assert flat_splits_for(8, 4, 256, 1) == 128
-    assert flat_splits_for(2, 20, 256, 2) == 512      # group 20: two head tiles
+    assert flat_splits_for(2, 20, 256, 2) == 256      # group 20: two head tiles
     assert flat_splits_for(64, 1, 4, 1) == 1
     # every BASELINE split shape takes the flat split ...
-    assert plan_decode([4096] * 64, 8, 4, 256, 2) == (1, 4096, 256)
-    assert plan_decode([16384] * 32, 8, 8, 256, 3) == (1, 16384, 256)
-    assert plan_decode([131072] * 4, 8, 4, 256, 2) == (1, 131072, 256)
+    assert plan_decode([4096] * 64, 8, 4, 256, 2) == (1, 4096, 128)
+    assert plan_decode([16384] * 32, 8, 8, 256, 3) == (1, 16384, 128)
+    assert plan_decode([131072] * 4, 8, 4, 256, 2) == (1, 131072, 128)
     # ... and a latency-bound batch (too few tiles per wave) the classic path
     s, m, f = plan_decode([192] * 24, 2, 7, 256, 4)
     assert f == 0 and s >= 1 and m == 192
@@ -352,7 +353,7 @@ def test_flat_splits_for_and_plan_decode():
     # batches above FLAT_MAX_BATCH take the classic planner
     from pagedattn.hip_decode import FLAT_MAX_BATCH
     assert plan_decode([4096] * (FLAT_MAX_BATCH + 1), 8, 4, 256, 2)[2] == 0
-    assert plan_decode([4096] * FLAT_MAX_BATCH, 8, 4, 256, 2)[2] == 256
+    assert plan_decode([4096] * FLAT_MAX_BATCH, 8, 4, 256, 2)[2] == 128
     # the threshold: MIN_FLAT_TILES_PER_WAVE tiles per wave
     from pagedattn.hip_decode import MIN_FLAT_TILES_PER_WAVE
     f = flat_splits_for(1, 1, 1, 1)
