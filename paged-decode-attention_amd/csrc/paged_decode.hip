@@ -74,7 +74,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWaves = 4;          // waves per workgroup (unsplit / classic split)
-constexpr int kMaxFlatWaves = 8;   // the widest flat-kernel workgroup
+constexpr int kFlatWaves = 4;      // flat kernel: one wave per SIMD of a CU
 constexpr int kSplitAlign = 32;    // split ranges are multiples of this many tokens
 constexpr float kRescaleLog2 = 8.0f;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -287,9 +287,6 @@ struct Geo {
   // largest instance that measured best double-buffered: fp16 at D = 128)
   static constexpr int kTileWords = 4 * kKLoads + kVRows * kVWords;
   static constexpr bool kPrefetch = 2 * kTileWords + 4 * kE + 4 * kKSteps <= 176;
-  // Flat-kernel workgroup: one wave per SIMD of a CU, on 4 neighbouring kv
-  // heads (the flat split launches one such workgroup per CU).
-  static constexpr int kFlatWaves = 4;
 };
 
 // Registers of one tile of one wave.
@@ -1016,11 +1013,13 @@ __device__ __forceinline__ void cursor_next(SeqCursor &cur, const ro_i32 *seq_le
 // register budget is still that of two waves per SIMD, the budget every
 // instance was tuned under.
 template <int KV, int SC, int D>
-__global__ void __launch_bounds__((Geo<KV, D>::kFlatWaves * 64)) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ void __launch_bounds__(kFlatWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
 paged_decode_flat_kernel(const KParams p) {
   using G = Geo<KV, D>;
   static_assert(G::kTT == kSplitAlign, "flat tiles are the kernel's tiles");
-  constexpr int W = G::kFlatWaves;
+  // the workgroup's waves take 4 neighbouring kv heads of one range, so
+  // together they read a contiguous 4-head stretch of every token row
+  constexpr int W = kFlatWaves;
   __shared__ __attribute__((aligned(16))) uint8_t sm_k[W * G::kKSlotBytes];
   __shared__ __attribute__((aligned(16))) float sm_sc[W][G::kScales];
 
@@ -1406,7 +1405,7 @@ int build_params(const pa_decode_args *a, bool need_partials, KParams *kp) {
     const int64_t seq_tiles_max = ((int64_t)a->max_blocks * a->block_size + kSplitAlign - 1) / kSplitAlign;
     if ((int64_t)a->batch * seq_tiles_max + a->flat_splits > 0x7fffffff)
       return fail(PA_ERR_UNSUPPORTED, "batch * max tiles per sequence too large for the flat split");
-    if ((int64_t)a->num_kv_heads * head_tiles * a->flat_splits + kMaxFlatWaves > 0x7fffffff)
+    if ((int64_t)a->num_kv_heads * head_tiles * a->flat_splits + kFlatWaves > 0x7fffffff)
       return fail(PA_ERR_UNSUPPORTED, "flat split grid too large");
   }
 
@@ -1460,7 +1459,7 @@ template <int KV, int SC, int D>
 hipError_t launch_decode_t(const KParams &k, int grid, int mode, hipStream_t st) {
   const dim3 g(grid), blk(kWaves * 64);
   if (mode == kFlat) {
-    constexpr int W = Geo<KV, D>::kFlatWaves;
+    constexpr int W = kFlatWaves;
     const int flat_grid = (k.hkv * k.head_tiles * k.flat_splits + W - 1) / W;
     hipLaunchKernelGGL((paged_decode_flat_kernel<KV, SC, D>), dim3(flat_grid), dim3(W * 64), 0, st, k);
   } else if (mode == kAuto) {
@@ -1657,25 +1656,20 @@ int pa_flat_waves_per_simd(int kv_dtype, int scale_dtype, int head_dim, int *out
   if (head_dim != 32 && head_dim != 64 && head_dim != 128 && head_dim != 256)
     return fail(PA_ERR_UNSUPPORTED, "head_dim %d not in (32, 64, 128, 256)", head_dim);
   const void *fn = nullptr;
-  int waves = 0;  // the kernel's workgroup width
   auto pick = [&](auto kv_tag, auto sc_tag) {
     constexpr int KV = decltype(kv_tag)::value, SC = decltype(sc_tag)::value;
     switch (head_dim) {
       case 32:
         fn = reinterpret_cast<const void *>(&paged_decode_flat_kernel<KV, SC, 32>);
-        waves = Geo<KV, 32>::kFlatWaves;
         break;
       case 64:
         fn = reinterpret_cast<const void *>(&paged_decode_flat_kernel<KV, SC, 64>);
-        waves = Geo<KV, 64>::kFlatWaves;
         break;
       case 128:
         fn = reinterpret_cast<const void *>(&paged_decode_flat_kernel<KV, SC, 128>);
-        waves = Geo<KV, 128>::kFlatWaves;
         break;
       default:
         fn = reinterpret_cast<const void *>(&paged_decode_flat_kernel<KV, SC, 256>);
-        waves = Geo<KV, 256>::kFlatWaves;
         break;
     }
   };
@@ -1694,9 +1688,9 @@ int pa_flat_waves_per_simd(int kv_dtype, int scale_dtype, int head_dim, int *out
     return fail(PA_ERR_INVALID, "kv_dtype %d / scale_dtype %d is not a supported pair", kv_dtype,
                 scale_dtype);
   int n = 0;
-  const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, waves * 64, 0);
+  const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kFlatWaves * 64, 0);
   if (e != hipSuccess) return fail(PA_ERR_HIP, "occupancy query failed: %s", hipGetErrorString(e));
-  *out = n * waves / 4;  // workgroups per CU -> waves per SIMD (4 SIMDs per CU)
+  *out = n * kFlatWaves / 4;  // workgroups per CU -> waves per SIMD (4 SIMDs per CU)
   return ok();
 }
 

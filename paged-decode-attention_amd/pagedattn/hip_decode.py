@@ -51,10 +51,6 @@ MIN_FLAT_TILES_PER_WAVE = 4
 # loads per lane: above this batch the classic split is used instead (such
 # batches fill the GPU unsplit anyway).
 FLAT_MAX_BATCH = 512
-# Flat-kernel waves per SIMD when the library cannot be asked (no GPU): the
-# gfx950 build's occupancy by (bytes per stored element, head_dim).
-_FLAT_WAVES_FALLBACK = {(2, 32): 4, (2, 64): 4, (2, 128): 2, (2, 256): 2,
-                        (1, 32): 4, (1, 64): 4, (1, 128): 2, (1, 256): 2}
 
 _KV_CODE = {"fp16": _abi.PA_KV_FP16, "fp8_e5m2": _abi.PA_KV_FP8_E5M2, "int8": _abi.PA_KV_INT8,
             "bf16": _abi.PA_KV_BF16}
@@ -185,7 +181,7 @@ _FLAT_WGS: dict[tuple, int] = {}
 
 def flat_waves_per_simd(kv_dtype: str, head_dim: int, scale_dtype: torch.dtype | None = None) -> int:
     """Resident flat-kernel waves per SIMD, from the library's occupancy
-    query on the current device (a built-in table without a GPU)."""
+    query on the current device (FLAT_WAVES_PER_SIMD without a GPU)."""
     sc = _abi.PA_SCALE_NONE if kv_dtype != "int8" else _SCALE_CODE.get(scale_dtype or torch.float16)
     key = (kv_dtype, head_dim, sc)
     n = _FLAT_WGS.get(key)
@@ -196,8 +192,9 @@ def flat_waves_per_simd(kv_dtype: str, head_dim: int, scale_dtype: torch.dtype |
             if _abi.load().pa_flat_waves_per_simd(_KV_CODE[kv_dtype], sc, head_dim, ctypes.byref(got)) == 0:
                 n = got.value
         if n <= 0:
-            elem = 2 if kv_dtype in ("fp16", "bf16") else 1
-            n = _FLAT_WAVES_FALLBACK.get((elem, head_dim), 2)
+            # every gfx950 instance holds at least the one wave per SIMD the
+            # flat split launches (occupancy 2 to 5)
+            n = FLAT_WAVES_PER_SIMD
         _FLAT_WGS[key] = n
     return n
 

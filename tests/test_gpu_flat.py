@@ -147,15 +147,15 @@ def test_flat_partial_slots_match_oracle(flat):
                                                   ("int8", torch.float16), ("int8", torch.float32)])
 @pytest.mark.parametrize("d", [32, 64, 128, 256])
 def test_flat_occupancy_query(kv_dtype, scale_dtype, d):
-    """The library's occupancy answer sizes flat_splits; the size it gives
-    must equal the one the no-GPU fallback table gives."""
-    from pagedattn.hip_decode import _FLAT_WAVES_FALLBACK, flat_splits_for, flat_waves_per_simd
+    """The library's occupancy answer sizes flat_splits; every instance holds
+    the one wave per SIMD the flat split launches, so the size equals the
+    one the planner uses without a GPU."""
+    from pagedattn.hip_decode import FLAT_WAVES_PER_SIMD, flat_splits_for, flat_waves_per_simd
 
     n = flat_waves_per_simd(kv_dtype, d, scale_dtype)
-    print(f"{kv_dtype} d={d}: {n} workgroups/CU")
-    assert 1 <= n <= 8
-    table = _FLAT_WAVES_FALLBACK[(2 if kv_dtype in ("fp16", "bf16") else 1, d)]
-    assert flat_splits_for(8, 4, 256, n) == flat_splits_for(8, 4, 256, table)
+    print(f"{kv_dtype} d={d}: {n} waves/SIMD")
+    assert FLAT_WAVES_PER_SIMD <= n <= 8
+    assert flat_splits_for(8, 4, 256, n) == flat_splits_for(8, 4, 256, FLAT_WAVES_PER_SIMD)
 
 
 def test_flat_partials_then_merge_equals_decode():
