@@ -310,7 +310,8 @@ def main() -> int:
     # unless --splits / --flat force a launch shape
     wps = flat_waves_per_simd(wl.kv_dtype, shape.head_dim,
                                  torch.float32 if wl.scale_fp32 else torch.float16)
-    splits, _, flat = plan_decode(wl.lens, shape.num_kv_heads, shape.gqa_group, cus, wps)
+    splits, _, flat = plan_decode(wl.lens, shape.num_kv_heads, shape.gqa_group, cus, wps,
+                                  kv_dtype=wl.kv_dtype, head_dim=shape.head_dim)
     if args.flat is not None or args.splits:
         flat = int(args.flat or 0)
         splits = 1 if flat else (args.splits or
@@ -462,7 +463,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {"fp16": "fp16", "fp8_e5m2": "fp8_e5m2", "int8": "int8"}[wl.kv_dtype],
+        "dtype": wl.kv_dtype,
         "data": "synthetic (seeded N(0,1) fp16 K/V/q, permuted block pool)",
         "config": {
             "workload": f"{wl.name}: {wl.description}",

@@ -47,6 +47,16 @@ SPLIT_ROUNDS = 2
 # 32-token tiles; smaller batches are latency-bound and run faster unsplit.
 FLAT_WAVES_PER_SIMD = 1
 MIN_FLAT_TILES_PER_WAVE = 4
+# A nearly uniform batch that fills the CUs unsplit (plan_num_splits gives
+# 1) runs unsplit while its K/V is at most this many bytes: the flat pass
+# streams faster but adds its merge launch (about 4 us). Whole-call
+# break-even measured at the Llama-3-8B shape (B = 64, g = 4, D = 128, 256
+# CUs), unsplit against flat: 2-byte KV 44.4 / 46.9 us at 268 MB, 85.2 / 85.1
+# at 537 MB, 166 / 162 at 1074 MB; fp8 26.6 / 29.0 at 134 MB, 49.5 / 47.2 at
+# 268 MB; int8 18.2 / 19.5 at 67 MB, 24.5 / 24.6 at 101 MB, 31.4 / 29.6 at
+# 134 MB.
+UNSPLIT_MAX_KV_BYTES = {"fp16": 512 << 20, "bf16": 512 << 20, "fp8_e5m2": 192 << 20,
+                        "int8": 96 << 20}
 # Every flat wave (and every merge wave) scans seq_lens once, batch / 64
 # loads per lane: above this batch the classic split is used instead (such
 # batches fill the GPU unsplit anyway).
@@ -125,20 +135,29 @@ def flat_splits_for(num_kv_heads: int, group: int, sm_count: int, waves_per_simd
 
 
 def plan_decode(seq_lens, num_kv_heads: int, group: int, sm_count: int,
-                waves_per_simd: int = 2) -> tuple[int, int, int]:
+                waves_per_simd: int = 1, kv_dtype: str | None = None,
+                head_dim: int | None = None) -> tuple[int, int, int]:
     """(num_splits, max_seq_len, flat_splits) for a batch whose lengths the host knows.
 
     The flat split (one round of waves, `flat_splits_for`) whenever each of
     its waves gets at least MIN_FLAT_TILES_PER_WAVE tiles and the batch is at
     most FLAT_MAX_BATCH: it is balanced for any mix of lengths and measured
-    fastest on every BASELINE split shape. Smaller batches take
-    `plan_num_splits`.
+    fastest on every BASELINE split shape. Exception, when `kv_dtype` and
+    `head_dim` are given: a nearly uniform batch that fills the CUs unsplit
+    stays unsplit (no merge launch) up to UNSPLIT_MAX_KV_BYTES of K/V.
+    Smaller batches take `plan_num_splits`.
     """
     lens = [max(0, int(t)) for t in seq_lens]
     tmax = max(lens) if lens else 0
     flat = flat_splits_for(num_kv_heads, group, sm_count, waves_per_simd)
     tiles = sum(-(-t // TILE_TOKENS) for t in lens)
     if len(lens) <= FLAT_MAX_BATCH and tiles >= MIN_FLAT_TILES_PER_WAVE * flat:
+        if kv_dtype is not None and head_dim is not None:
+            elem = 1 if kv_dtype in ("fp8_e5m2", "int8") else 2
+            kv_bytes = sum(lens) * num_kv_heads * head_dim * elem * 2
+            if (kv_bytes <= UNSPLIT_MAX_KV_BYTES.get(kv_dtype, 0)
+                    and plan_num_splits(lens, num_kv_heads, group, sm_count)[0] == 1):
+                return 1, tmax, 0
         return 1, tmax, flat
     splits, tmax = plan_num_splits(lens, num_kv_heads, group, sm_count)
     return splits, tmax, 0
@@ -378,7 +397,8 @@ def paged_decode_hip(
         # the lengths come to the host in the one sync the reference also makes
         wps = flat_waves_per_simd(cache.kv_dtype, d, None if cache.k_scale is None else cache.k_scale.dtype)
         num_splits, longest, flat_splits = plan_decode(cache.seq_lens.tolist(), hkv, group,
-                                                       _cu_count(q.device), wps)
+                                                       _cu_count(q.device), wps,
+                                                       kv_dtype=cache.kv_dtype, head_dim=d)
         if max_seq_len is None:
             max_seq_len = longest
     num_splits = int(num_splits)

@@ -354,6 +354,20 @@ def test_flat_splits_for_and_plan_decode():
     from pagedattn.hip_decode import FLAT_MAX_BATCH
     assert plan_decode([4096] * (FLAT_MAX_BATCH + 1), 8, 4, 256, 2)[2] == 0
     assert plan_decode([4096] * FLAT_MAX_BATCH, 8, 4, 256, 2)[2] == 128
+    # with the KV type known, a nearly uniform batch that fills the CUs
+    # unsplit stays unsplit while its K/V is small (no merge launch) ...
+    assert plan_decode([1024] * 64, 8, 4, 256, 1, kv_dtype="fp16", head_dim=128) == (1, 1024, 0)
+    assert plan_decode([1024] * 64, 8, 4, 256, 1, kv_dtype="bf16", head_dim=128) == (1, 1024, 0)
+    assert plan_decode([1024] * 64, 8, 4, 256, 1, kv_dtype="fp8_e5m2", head_dim=128) == (1, 1024, 0)
+    assert plan_decode([512] * 64, 8, 4, 256, 1, kv_dtype="int8", head_dim=128) == (1, 512, 0)
+    # ... and above the per-type byte limit takes the flat split
+    assert plan_decode([4096] * 64, 8, 4, 256, 1, kv_dtype="fp16", head_dim=128)[2] == 128
+    assert plan_decode([2048] * 64, 8, 4, 256, 1, kv_dtype="fp8_e5m2", head_dim=128)[2] == 128
+    assert plan_decode([1024] * 64, 8, 4, 256, 1, kv_dtype="int8", head_dim=128)[2] == 128
+    # a ragged batch of the same size, or one that does not fill the CUs, too
+    ragged = [256, 1792] * 32
+    assert plan_decode(ragged, 8, 4, 256, 1, kv_dtype="fp16", head_dim=128)[2] == 128
+    assert plan_decode([8192] * 8, 8, 4, 256, 1, kv_dtype="fp16", head_dim=128)[2] == 128
     # the threshold: MIN_FLAT_TILES_PER_WAVE tiles per wave
     from pagedattn.hip_decode import MIN_FLAT_TILES_PER_WAVE
     f = flat_splits_for(1, 1, 1, 1)
