@@ -12,6 +12,7 @@ from .cache import PagedKVCache, allocate, quantize_kv
 from .cache_ops import reshape_and_cache
 from .hip_decode import (
     decode_partials,
+    flat_needs_merge,
     flat_splits_for,
     flat_waves_per_simd,
     paged_decode_hip,
@@ -27,6 +28,6 @@ __all__ = [
     "kv_bytes_per_token",
     "PagedKVCache", "allocate", "quantize_kv", "reshape_and_cache",
     "paged_decode_hip", "paged_decode_triton", "pick_num_splits", "plan_num_splits",
-    "plan_decode", "flat_splits_for", "flat_waves_per_simd",
+    "plan_decode", "flat_needs_merge", "flat_splits_for", "flat_waves_per_simd",
     "decode_partials", "split_reduce",
 ]

@@ -163,6 +163,32 @@ def plan_decode(seq_lens, num_kv_heads: int, group: int, sm_count: int,
     return splits, tmax, 0
 
 
+def flat_needs_merge(seq_lens, flat_splits: int, max_tokens: int | None = None) -> bool:
+    """Whether a flat decode over these lengths leaves work to its merge pass.
+
+    It does when a range boundary cuts a sequence (its pieces are partials)
+    or a sequence is empty (the merge writes its zeros). Otherwise every
+    sequence lies inside one range and the decode pass writes all of `out`
+    itself, as for a uniform batch whose length in tiles times the batch
+    divides evenly among the ranges. Lengths are clamped to `max_tokens` (the
+    block table's capacity), as the kernels clamp them.
+    """
+    lens = [max(0, int(t)) for t in seq_lens]
+    if max_tokens is not None:
+        lens = [min(t, max_tokens) for t in lens]
+    tiles = [-(-t // TILE_TOKENS) for t in lens]
+    total = sum(tiles)
+    if total == 0 or flat_splits <= 0:
+        return True
+    per = max(1, -(-total // flat_splits))
+    cu = 0
+    for n in tiles:
+        if n == 0 or cu // per != (cu + n - 1) // per:
+            return True
+        cu += n
+    return False
+
+
 class _Workspace:
     """Split-KV scratch (fp32 partial outputs and log2-sum-exps), per device.
 
@@ -391,16 +417,19 @@ def paged_decode_hip(
         out = torch.empty((b, hq, d), dtype=q.dtype, device=q.device)
     if b == 0:
         return out
+    merge = True  # a flat decode runs its merge pass
     if flat_splits:
         num_splits = 1
     elif num_splits is None:
         # the lengths come to the host in the one sync the reference also makes
+        lens = cache.seq_lens.tolist()
         wps = flat_waves_per_simd(cache.kv_dtype, d, None if cache.k_scale is None else cache.k_scale.dtype)
-        num_splits, longest, flat_splits = plan_decode(cache.seq_lens.tolist(), hkv, group,
-                                                       _cu_count(q.device), wps,
+        num_splits, longest, flat_splits = plan_decode(lens, hkv, group, _cu_count(q.device), wps,
                                                        kv_dtype=cache.kv_dtype, head_dim=d)
         if max_seq_len is None:
             max_seq_len = longest
+        if flat_splits:
+            merge = flat_needs_merge(lens, flat_splits, cache.block_table.shape[1] * cache.block_size)
     num_splits = int(num_splits)
     scale = shape.softmax_scale if sm_scale is None else float(sm_scale)
 
@@ -413,6 +442,11 @@ def paged_decode_hip(
         part_out, part_lse = _WS.get(b, hq, num_splits, d, q.device)
     args = _fill_args(q, cache, out, num_splits, scale, part_out, part_lse, max_seq_len or 0, flat)
     lib = _abi.load()
+    if flat > 0 and not merge:
+        # every sequence inside one range: the decode pass writes all of out
+        rc = _call(q.device, lib.pa_decode_partials, ctypes.byref(args), _stream(q.device))
+        _abi.check(rc, "pa_decode_partials")
+        return out
     rc = _call(q.device, lib.pa_decode, ctypes.byref(args), _stream(q.device))
     _abi.check(rc, "pa_decode")
     return out
@@ -530,6 +564,7 @@ __all__ = [
     "split_count_for",
     "plan_num_splits",
     "plan_decode",
+    "flat_needs_merge",
     "flat_splits_for",
     "flat_waves_per_simd",
     "WAVES_PER_WORKGROUP",

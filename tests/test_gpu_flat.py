@@ -273,3 +273,30 @@ def test_out_of_range_lengths_and_block_ids_are_clamped(kw):
     want = oracle.reference_decode(q, good, out_dtype=torch.float32)
     assert max_abs(got[:3], want[:3]) < ABS_TOL
     assert torch.equal(got[3].cpu(), torch.zeros_like(got[3].cpu()))
+
+
+def test_aligned_flat_batch_skips_the_merge():
+    """A uniform batch whose ranges each hold whole sequences (B = 128 at
+    T = 2048: one sequence per range at F = 128) runs the decode pass alone
+    when the split is planned from the lengths; the result is bit-identical
+    to the flat decode with its merge launched, and matches the oracle."""
+    from helpers import subset_cache
+    from pagedattn import flat_needs_merge, flat_splits_for, flat_waves_per_simd, plan_decode
+    from pagedattn.hip_decode import _cu_count
+
+    lens = [2048] * 128
+    c = allocate(LLAMA3_8B, len(lens), lens, seed=41, device="cuda", fill_device="cuda")
+    q = seeded_q(len(lens), 32, 128, 41, device="cuda")
+    cus = _cu_count(q.device)
+    flat = flat_splits_for(8, 4, cus, flat_waves_per_simd("fp16", 128))
+    planned = plan_decode(lens, 8, 4, cus, 1, kv_dtype="fp16", head_dim=128)
+    print(f"plan {planned}, needs merge {flat_needs_merge(lens, flat)}")
+    if planned[2] == 0 or flat_needs_merge(lens, planned[2]):
+        pytest.skip(f"{cus} CUs: the plan {planned} is not a merge-free flat split")
+    auto = paged_decode_hip(q, c).clone()
+    explicit = paged_decode_hip(q, c, flat_splits=planned[2])
+    torch.cuda.synchronize()
+    assert torch.equal(auto, explicit)
+    rows = [0, 77, 127]
+    want = oracle.reference_decode(q[rows].cpu(), subset_cache(c, rows), out_dtype=torch.float32)
+    assert max_abs(auto[rows], want) < ABS_TOL

@@ -626,3 +626,39 @@ def test_bf16_rows_are_read_as_fp16():
     assert torch.equal(out[0, 0, :4], want)
     got_c = c_oracle.decode(q, c).float()
     assert torch.equal(got_c[0, 0, :4], want)
+
+
+def test_flat_needs_merge_agrees_with_the_oracle_work_list():
+    """The host's merge-free test (pagedattn.flat_needs_merge) against the
+    oracle's restatement of the flat work list: no merge exactly when every
+    sequence is one segment of one range."""
+    import random
+
+    from pagedattn import flat_needs_merge
+
+    def oracle_needs(lens, flat, max_tokens=None):
+        if max_tokens is not None:
+            lens = [min(t, max_tokens) for t in lens]
+        segs, _ = oracle.flat_segments(lens, flat)
+        count = [0] * len(lens)
+        for _, b, _, _ in segs:
+            count[b] += 1
+        return any(c != 1 for c in count)
+
+    # known answers
+    assert not flat_needs_merge([2048] * 128, 128)      # one sequence per range
+    assert not flat_needs_merge([2048] * 256, 128)      # two per range
+    assert flat_needs_merge([2048] * 64, 128)           # two ranges per sequence
+    assert not flat_needs_merge([100] * 16, 16)
+    assert flat_needs_merge([100] * 15 + [0], 16)       # an empty sequence: merge writes zeros
+    assert flat_needs_merge([], 4) and flat_needs_merge([0, 0], 4)
+    assert not flat_needs_merge([4096, 5000], 2, max_tokens=4096)   # clamped to 128 tiles each
+    assert flat_needs_merge([4096, 5000], 2)                       # 128 + 157 tiles: cut
+    rng = random.Random(5)
+    for _ in range(500):
+        lens = [rng.choice([0, 1, 31, 32, 33, 64, 100, 4096]) if rng.random() < 0.3 else rng.randint(0, 700)
+                for _ in range(rng.randint(1, 20))]
+        flat = rng.randint(1, 40)
+        assert flat_needs_merge(lens, flat) == oracle_needs(lens, flat), (lens, flat)
+        cap = rng.choice([32, 64, 512])
+        assert flat_needs_merge(lens, flat, cap) == oracle_needs(lens, flat, cap), (lens, flat, cap)
