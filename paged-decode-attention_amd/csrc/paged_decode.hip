@@ -1018,7 +1018,8 @@ paged_decode_flat_kernel(const KParams p) {
   using G = Geo<KV, D>;
   static_assert(G::kTT == kSplitAlign, "flat tiles are the kernel's tiles");
   // the workgroup's waves take 4 neighbouring kv heads of one range, so
-  // together they read a contiguous 4-head stretch of every token row
+  // together they read a contiguous 4-head stretch of every token row (4
+  // consecutive ranges of one kv head instead ran 8-14% slower)
   constexpr int W = kFlatWaves;
   __shared__ __attribute__((aligned(16))) uint8_t sm_k[W * G::kKSlotBytes];
   __shared__ __attribute__((aligned(16))) float sm_sc[W][G::kScales];
