@@ -144,15 +144,16 @@ def plan_decode(seq_lens, num_kv_heads: int, group: int, sm_count: int,
     most FLAT_MAX_BATCH: it is balanced for any mix of lengths and measured
     fastest on every BASELINE split shape. Exception, when `kv_dtype` and
     `head_dim` are given: a nearly uniform batch that fills the CUs unsplit
-    stays unsplit (no merge launch) up to UNSPLIT_MAX_KV_BYTES of K/V.
-    Smaller batches take `plan_num_splits`.
+    stays unsplit (no merge launch) up to UNSPLIT_MAX_KV_BYTES of K/V, unless
+    the flat split needs no merge either (`flat_needs_merge`), as for a
+    uniform batch of 128 at F = 128. Smaller batches take `plan_num_splits`.
     """
     lens = [max(0, int(t)) for t in seq_lens]
     tmax = max(lens) if lens else 0
     flat = flat_splits_for(num_kv_heads, group, sm_count, waves_per_simd)
     tiles = sum(-(-t // TILE_TOKENS) for t in lens)
     if len(lens) <= FLAT_MAX_BATCH and tiles >= MIN_FLAT_TILES_PER_WAVE * flat:
-        if kv_dtype is not None and head_dim is not None:
+        if kv_dtype is not None and head_dim is not None and flat_needs_merge(lens, flat):
             elem = 1 if kv_dtype in ("fp8_e5m2", "int8") else 2
             kv_bytes = sum(lens) * num_kv_heads * head_dim * elem * 2
             if (kv_bytes <= UNSPLIT_MAX_KV_BYTES.get(kv_dtype, 0)
