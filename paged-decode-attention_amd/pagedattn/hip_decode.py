@@ -9,8 +9,8 @@ if the library is missing or the tensors are not on a GPU, the call raises.
 Knobs of the reference that only steer Triton code generation (`per_page_bt`,
 `num_warps`, `num_stages`) are accepted and ignored: the HIP kernels always
 read one block-table entry per 16-token sub-tile (one per page at page size
-16) and size their workgroups themselves (4 waves; the flat kernel 4 or 8 by
-row width). `block_n` keeps the reference's check that it is a multiple of
+16) and size their workgroups themselves (4 waves; the flat kernel's are one
+wave per SIMD of a CU). `block_n` keeps the reference's check that it is a multiple of
 the page size; split ranges are aligned to the kernels' 32-token tile.
 """
 
@@ -222,7 +222,7 @@ class _Workspace:
 
 _WS = _Workspace()
 _CU_COUNT: dict[int, int] = {}
-_FLAT_WGS: dict[tuple, int] = {}
+_FLAT_WPS: dict[tuple, int] = {}
 
 
 def flat_waves_per_simd(kv_dtype: str, head_dim: int, scale_dtype: torch.dtype | None = None) -> int:
@@ -230,7 +230,7 @@ def flat_waves_per_simd(kv_dtype: str, head_dim: int, scale_dtype: torch.dtype |
     query on the current device (FLAT_WAVES_PER_SIMD without a GPU)."""
     sc = _abi.PA_SCALE_NONE if kv_dtype != "int8" else _SCALE_CODE.get(scale_dtype or torch.float16)
     key = (kv_dtype, head_dim, sc)
-    n = _FLAT_WGS.get(key)
+    n = _FLAT_WPS.get(key)
     if n is None:
         n = 0
         if torch.cuda.is_available() and kv_dtype in _KV_CODE:
@@ -241,7 +241,7 @@ def flat_waves_per_simd(kv_dtype: str, head_dim: int, scale_dtype: torch.dtype |
             # every gfx950 instance holds at least the one wave per SIMD the
             # flat split launches (occupancy 2 to 5)
             n = FLAT_WAVES_PER_SIMD
-        _FLAT_WGS[key] = n
+        _FLAT_WPS[key] = n
     return n
 
 
