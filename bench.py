@@ -129,8 +129,10 @@ def cpu_baseline(q, cache, budget_s: float) -> dict:
     t0 = time.perf_counter()
     oracle.reference_decode(q[:1].cpu(), probe)
     per_seq = max(time.perf_counter() - t0, 1e-4)
-    runs = 3
-    n = int(max(1, min(b, budget_s / (runs * per_seq))))
+    # as many sequences as three runs fit in the budget, then as many runs
+    # (3 to 15) as the budget holds, for a stable median
+    n = int(max(1, min(b, budget_s / (3 * per_seq))))
+    runs = int(max(3, min(15, budget_s / (n * per_seq))))
     rows = list(range(n))
     sub = subset_cache(cache, rows)
     qs = q[:n].cpu()
