@@ -1,0 +1,85 @@
+"""Seeded random sweep of the decode against the CPU oracle.
+
+Each case draws a head geometry, head_dim, KV dtype (with fp16 or fp32 int8
+scales), page size, batch and ragged lengths (empty and 1-token sequences
+included), q/out dtype and a launch shape: unsplit, the reference's
+per-sequence split (with and without `max_seq_len`), the flat split at a random
+range count, or the planner's choice (`num_splits=None`). Every case is held
+to the decode's bar against the fp32 oracle (pagedattn/reference.py:28-49
+restated): max |HIP - oracle| < 2e-3 (plus one bf16 rounding for bf16 out),
+and zeros for empty sequences.
+"""
+
+from __future__ import annotations
+
+import random
+
+import pytest
+import torch
+
+from helpers import seeded_q
+from oracle import reference as oracle
+from pagedattn import ModelShape, allocate
+from pagedattn.hip_decode import paged_decode_hip
+
+pytestmark = pytest.mark.gpu
+
+ABS_TOL = 2e-3
+GEOMETRIES = [(32, 8), (64, 8), (14, 2), (8, 8), (40, 2), (16, 1), (12, 4), (28, 4)]
+CASES = 48
+
+
+def _draw(seed):
+    rng = random.Random(seed)
+    hq, hkv = rng.choice(GEOMETRIES)
+    d = rng.choice([32, 64, 128, 128, 256])
+    kv = rng.choice(["fp16", "bf16", "fp8_e5m2", "int8", "int8"])
+    sdt = rng.choice([torch.float16, torch.float32])
+    page = rng.choice([16, 16, 32, 64])
+    b = rng.choice([1, 2, 3, 5, 8, 13, 24, 40, 70])
+    lens = []
+    for _ in range(b):
+        r = rng.random()
+        lens.append(0 if r < 0.08 else 1 if r < 0.14 else rng.randint(2, 600) if r < 0.8
+                    else rng.randint(600, 3000))
+    io = rng.choice([torch.float16, torch.float16, torch.bfloat16])
+    mode = rng.choice(["unsplit", "split", "split_msl", "flat", "flat", "auto"])
+    knob = rng.randint(2, 9) if mode.startswith("split") else rng.randint(1, 300)
+    return hq, hkv, d, kv, sdt, page, lens, io, mode, knob
+
+
+@pytest.mark.parametrize("case", range(CASES))
+def test_random_case(case):
+    run_case(1000 + case)
+
+
+def run_case(case):
+    hq, hkv, d, kv, sdt, page, lens, io, mode, knob = _draw(case)
+    print(f"case {case}: hq={hq} hkv={hkv} d={d} kv={kv} scales={sdt} page={page} "
+          f"B={len(lens)} max_len={max(lens)} io={io} mode={mode} knob={knob}", flush=True)
+    shape = ModelShape(hq, hkv, d, name="sweep")
+    c = allocate(shape, len(lens), lens, block_size=page, kv_dtype=kv, seed=case,
+                 scale_dtype=sdt, device="cuda")
+    q = seeded_q(len(lens), hq, d, case, device="cuda").to(io)
+    kw = {"block_n": max(64, page)}
+    if mode == "unsplit":
+        kw["num_splits"] = 1
+    elif mode == "split":
+        kw["num_splits"] = knob
+    elif mode == "split_msl":
+        kw.update(num_splits=knob, max_seq_len=max(lens))
+    elif mode == "flat":
+        kw["flat_splits"] = knob
+    got = paged_decode_hip(q, c, **kw)
+    torch.cuda.synchronize()
+    want = oracle.reference_decode(q, c, out_dtype=torch.float32)
+    live = [i for i, t in enumerate(lens) if t > 0]
+    dead = [i for i, t in enumerate(lens) if t == 0]
+    if live:
+        g, w = got[live].float().cpu(), want[live]
+        err = (g - w).abs()
+        bound = ABS_TOL + (2.0 ** -8 * w.abs() if io == torch.bfloat16 else 0.0)
+        print(f"  max_abs={err.max().item():.2e}", flush=True)
+        assert bool((err <= bound).all())
+    if dead:
+        assert torch.equal(got[dead].float().cpu(), torch.zeros((len(dead), hq, d)))
