@@ -59,8 +59,13 @@ UNSPLIT_MAX_KV_BYTES = {"fp16": 512 << 20, "bf16": 512 << 20, "fp8_e5m2": 192 <<
                         "int8": 96 << 20}
 # Every flat wave (and every merge wave) scans seq_lens once, batch / 64
 # loads per lane: above this batch the classic split is used instead (such
-# batches fill the GPU unsplit anyway).
+# batches fill the GPU unsplit anyway)...
 FLAT_MAX_BATCH = 512
+# ... unless the flat split needs no merge (every range holds whole
+# sequences): then only the decode waves scan, and up to this batch the flat
+# pass beats the unsplit kernel (B = 1024, T = 1024: fp16 661 against 683 us,
+# fp8 341 against 385, int8 352 against 421; at B = 2048 fp16 gains 1%).
+FLAT_MERGE_FREE_MAX_BATCH = 1024
 
 _KV_CODE = {"fp16": _abi.PA_KV_FP16, "fp8_e5m2": _abi.PA_KV_FP8_E5M2, "int8": _abi.PA_KV_INT8,
             "bf16": _abi.PA_KV_BF16}
@@ -142,7 +147,8 @@ def plan_decode(seq_lens, num_kv_heads: int, group: int, sm_count: int,
     The flat split (one round of waves, `flat_splits_for`) whenever each of
     its waves gets at least MIN_FLAT_TILES_PER_WAVE tiles and the batch is at
     most FLAT_MAX_BATCH: it is balanced for any mix of lengths and measured
-    fastest on every BASELINE split shape. Exception, when `kv_dtype` and
+    fastest on every BASELINE split shape (and, when it needs no merge, up to
+    FLAT_MERGE_FREE_MAX_BATCH sequences). Exception, when `kv_dtype` and
     `head_dim` are given: a nearly uniform batch that fills the CUs unsplit
     stays unsplit (no merge launch) up to UNSPLIT_MAX_KV_BYTES of K/V, unless
     the flat split needs no merge either (`flat_needs_merge`), as for a
@@ -152,7 +158,9 @@ def plan_decode(seq_lens, num_kv_heads: int, group: int, sm_count: int,
     tmax = max(lens) if lens else 0
     flat = flat_splits_for(num_kv_heads, group, sm_count, waves_per_simd)
     tiles = sum(-(-t // TILE_TOKENS) for t in lens)
-    if len(lens) <= FLAT_MAX_BATCH and tiles >= MIN_FLAT_TILES_PER_WAVE * flat:
+    fits = len(lens) <= FLAT_MAX_BATCH or (len(lens) <= FLAT_MERGE_FREE_MAX_BATCH
+                                           and not flat_needs_merge(lens, flat))
+    if fits and tiles >= MIN_FLAT_TILES_PER_WAVE * flat:
         if kv_dtype is not None and head_dim is not None and flat_needs_merge(lens, flat):
             elem = 1 if kv_dtype in ("fp8_e5m2", "int8") else 2
             kv_bytes = sum(lens) * num_kv_heads * head_dim * elem * 2

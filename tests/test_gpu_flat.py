@@ -300,3 +300,28 @@ def test_aligned_flat_batch_skips_the_merge():
     rows = [0, 77, 127]
     want = oracle.reference_decode(q[rows].cpu(), subset_cache(c, rows), out_dtype=torch.float32)
     assert max_abs(auto[rows], want) < ABS_TOL
+
+
+def test_large_uniform_batch_takes_the_merge_free_flat_split():
+    """B = 1024 (above FLAT_MAX_BATCH): each flat range holds 8 whole
+    sequences, so the planner takes the flat split and the decode pass alone
+    writes every output; it agrees with the unsplit kernel on every row and
+    with the oracle on sampled rows."""
+    from helpers import subset_cache
+    from pagedattn import flat_needs_merge, plan_decode
+    from pagedattn.hip_decode import _cu_count
+
+    lens = [256] * 1024
+    c = allocate(LLAMA3_8B, len(lens), lens, seed=43, device="cuda", fill_device="cuda")
+    q = seeded_q(len(lens), 32, 128, 43, device="cuda")
+    planned = plan_decode(lens, 8, 4, _cu_count(q.device), 1, kv_dtype="fp16", head_dim=128)
+    print(f"plan {planned}")
+    if planned[2] == 0 or flat_needs_merge(lens, planned[2]):
+        pytest.skip(f"the plan {planned} is not a merge-free flat split on this GPU")
+    auto = paged_decode_hip(q, c).clone()
+    unsplit = paged_decode_hip(q, c, num_splits=1)
+    torch.cuda.synchronize()
+    assert (auto.float() - unsplit.float()).abs().max().item() < ABS_TOL
+    rows = [0, 511, 1023]
+    want = oracle.reference_decode(q[rows].cpu(), subset_cache(c, rows), out_dtype=torch.float32)
+    assert max_abs(auto[rows], want) < ABS_TOL
