@@ -945,14 +945,43 @@ __device__ __forceinline__ int wave_incl_scan(int x, int lane) {
 
 // Total flat tiles of the batch (wave-uniform); `len0` receives this lane's
 // clamped length of sequence `lane` (0 past the batch).
+// seq_lens is scanned kLenChunks chunks of 64 at a time: the chunks' loads
+// are all issued before any is used, so up to 512 sequences cost one round
+// trip instead of one per 64 (16 chunks made the compiler raise every flat
+// instance to 230 VGPRs).
+constexpr int kLenChunks = 8;
+
+// Clamped lengths of sequences base + 64 k + lane (k < kLenChunks; 0 past the
+// batch), loaded together.
+__device__ __forceinline__ void load_len_chunks(const ro_i32 *seq_lens, int batch, int max_tokens,
+                                                int base, int lane, int (&len)[kLenChunks]) {
+#pragma unroll
+  for (int k = 0; k < kLenChunks; ++k) {
+    len[k] = 0;
+    if (base + 64 * k < batch) {  // wave-uniform
+      const int b = base + 64 * k + lane;
+      if (b < batch) len[k] = max(0, min(seq_lens[b], max_tokens));
+    }
+  }
+}
+
+__device__ __forceinline__ int len_tiles(int len) { return (len + kSplitAlign - 1) / kSplitAlign; }
+
 __device__ __forceinline__ int flat_total(const ro_i32 *seq_lens, int batch, int max_tokens,
                                           int lane, int &len0) {
+  if (batch <= 64) {  // one chunk
+    len0 = lane < batch ? max(0, min(seq_lens[lane], max_tokens)) : 0;
+    return __builtin_amdgcn_readfirstlane(wave_sum(len_tiles(len0)));
+  }
   int total = 0;
-  for (int base = 0; base < batch; base += 64) {
-    const int b = base + lane;
-    const int len = b < batch ? max(0, min(seq_lens[b], max_tokens)) : 0;
-    if (base == 0) len0 = len;
-    total += wave_sum((len + kSplitAlign - 1) / kSplitAlign);
+  for (int base = 0; base < batch; base += 64 * kLenChunks) {
+    int len[kLenChunks];
+    load_len_chunks(seq_lens, batch, max_tokens, base, lane, len);
+    if (base == 0) len0 = len[0];
+    int t = 0;
+#pragma unroll
+    for (int k = 0; k < kLenChunks; ++k) t += len_tiles(len[k]);
+    total += wave_sum(t);
   }
   return __builtin_amdgcn_readfirstlane(total);
 }
@@ -969,22 +998,44 @@ struct SeqCursor {
 __device__ __forceinline__ SeqCursor flat_locate(const ro_i32 *seq_lens, int batch, int max_tokens,
                                                  int f, int lane, int len0) {
   SeqCursor cur = {0, 0, 0, 0};
-  int run = 0;
-  for (int base = 0; base < batch; base += 64) {
-    const int b = base + lane;
-    const int len = (base == 0 && len0 >= 0) ? len0
-                    : b < batch ? max(0, min(seq_lens[b], max_tokens)) : 0;
-    const int t = (len + kSplitAlign - 1) / kSplitAlign;
-    const int incl = wave_incl_scan(t, lane) + run;
+  if (len0 >= 0) {  // batch <= 64: one chunk, already loaded
+    const int t = len_tiles(len0);
+    const int incl = wave_incl_scan(t, lane);
     const uint64_t hit = __builtin_amdgcn_ballot_w64(incl > f);
-    if (hit != 0) {
-      const int l = __builtin_ctzll(hit);
-      cur.b = base + l;
+    const int l = hit != 0 ? __builtin_ctzll(hit) : 0;
+    cur.b = l;
+    cur.t = f - __shfl(incl - t, l);
+    cur.len = __shfl(len0, l);
+  } else {
+    int run = 0;  // tiles of the sequences before this pass
+    for (int base = 0; base < batch; base += 64 * kLenChunks) {
+      int len[kLenChunks];
+      load_len_chunks(seq_lens, batch, max_tokens, base, lane, len);
+      // the chunk holding f, from the chunks' tile sums (wave-uniform) ...
+      int kk = -1;
+#pragma unroll
+      for (int k = 0; k < kLenChunks; ++k) {
+        const int ck = __builtin_amdgcn_readfirstlane(wave_sum(len_tiles(len[k])));
+        if (kk < 0) {
+          if (run + ck > f) kk = k;
+          else run += ck;
+        }
+      }
+      if (kk < 0) continue;
+      // ... then f's sequence inside that chunk
+      int lk = 0;
+#pragma unroll
+      for (int k = 0; k < kLenChunks; ++k)
+        if (k == kk) lk = len[k];
+      const int t = len_tiles(lk);
+      const int incl = wave_incl_scan(t, lane) + run;
+      const uint64_t hit = __builtin_amdgcn_ballot_w64(incl > f);
+      const int l = hit != 0 ? __builtin_ctzll(hit) : 0;
+      cur.b = base + 64 * kk + l;
       cur.t = f - __shfl(incl - t, l);
-      cur.len = __shfl(len, l);
+      cur.len = __shfl(lk, l);
       break;
     }
-    run = __shfl(incl, 63);
   }
   cur.b = __builtin_amdgcn_readfirstlane(cur.b);
   cur.t = __builtin_amdgcn_readfirstlane(cur.t);
@@ -1192,14 +1243,26 @@ __global__ void __launch_bounds__(kMergeWaves * 64) split_reduce_kernel(const RP
     if (S <= 1) return;
   } else if (KIND == kMergeFlat) {
     // the decode's ranges: per = ceil(total / F) flat tiles each
-    int total = 0, cu = 0;
-    for (int base = 0; base < p.batch; base += 64) {
-      const int bb = base + lane;
-      const int t = bb < p.batch ? seq_tiles(ro(p.seq_lens), bb, p.max_tokens) : 0;
-      total += wave_sum(t);
-      cu += wave_sum(bb < b ? t : 0);
-    }
     const int nt = seq_tiles(ro(p.seq_lens), b, p.max_tokens);
+    int total = 0, cu = 0;
+    if (p.batch <= 64) {  // one chunk
+      const int t = lane < p.batch ? seq_tiles(ro(p.seq_lens), lane, p.max_tokens) : 0;
+      total = wave_sum(t);
+      cu = wave_sum(lane < b ? t : 0);
+    }
+    for (int base = 0; base < p.batch && p.batch > 64; base += 64 * kLenChunks) {
+      int len[kLenChunks];
+      load_len_chunks(ro(p.seq_lens), p.batch, p.max_tokens, base, lane, len);
+      int t = 0, tb = 0;
+#pragma unroll
+      for (int k = 0; k < kLenChunks; ++k) {
+        const int tk = len_tiles(len[k]);
+        t += tk;
+        tb += base + 64 * k + lane < b ? tk : 0;
+      }
+      total += wave_sum(t);
+      cu += wave_sum(tb);
+    }
     S = 0;  // empty sequence: the merge below writes zeros
     if (nt > 0) {
       const int per = max(1, (total + p.num_splits - 1) / p.num_splits);
