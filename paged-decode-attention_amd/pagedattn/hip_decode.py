@@ -57,15 +57,18 @@ MIN_FLAT_TILES_PER_WAVE = 4
 # 134 MB.
 UNSPLIT_MAX_KV_BYTES = {"fp16": 512 << 20, "bf16": 512 << 20, "fp8_e5m2": 192 << 20,
                         "int8": 96 << 20}
-# Every flat wave (and every merge wave) scans seq_lens once, batch / 64
-# loads per lane: above this batch the classic split is used instead (such
-# batches fill the GPU unsplit anyway)...
-FLAT_MAX_BATCH = 512
+# Every flat wave and every merge wave scans seq_lens (512 lengths per round
+# trip), so the merge grows with the batch: above this batch the classic
+# kernel runs unsplit instead. Whole calls on ragged batches (T ~ U[256,
+# 2048]), flat against unsplit: B = 512 fp16 406 / 415 us, int8 224 / 264;
+# B = 1024 fp16 790 / 794, int8 434 / 490, fp8 425 / 451; B = 2048 fp16
+# 1596 / 1566 ...
+FLAT_MAX_BATCH = 1024
 # ... unless the flat split needs no merge (every range holds whole
-# sequences): then only the decode waves scan, and up to this batch the flat
-# pass beats the unsplit kernel (B = 1024, T = 1024: fp16 661 against 683 us,
-# fp8 341 against 385, int8 352 against 421; at B = 2048 fp16 gains 1%).
-FLAT_MERGE_FREE_MAX_BATCH = 1024
+# sequences): then only the decode waves scan, and the flat pass alone beats
+# the unsplit kernel up to this batch (B = 2048, T = 256: fp16 367 / 375 us,
+# int8 223 / 255; B = 4096, T = 128: fp16 399 / 469, int8 257 / 317).
+FLAT_MERGE_FREE_MAX_BATCH = 4096
 
 _KV_CODE = {"fp16": _abi.PA_KV_FP16, "fp8_e5m2": _abi.PA_KV_FP8_E5M2, "int8": _abi.PA_KV_INT8,
             "bf16": _abi.PA_KV_BF16}

@@ -325,3 +325,28 @@ def test_large_uniform_batch_takes_the_merge_free_flat_split():
     rows = [0, 511, 1023]
     want = oracle.reference_decode(q[rows].cpu(), subset_cache(c, rows), out_dtype=torch.float32)
     assert max_abs(auto[rows], want) < ABS_TOL
+
+
+def test_flat_ragged_batch_of_1000():
+    """A ragged batch of 1,000 (two 512-length passes of every seq_lens scan,
+    in the decode waves and in the merge) agrees with the unsplit kernel on
+    every row and with the oracle on sampled rows."""
+    import random
+
+    from helpers import subset_cache
+
+    rng = random.Random(44)
+    lens = [rng.choice([0, 1, 17]) if rng.random() < 0.05 else rng.randint(2, 400) for _ in range(1000)]
+    c = allocate(LLAMA3_8B, len(lens), lens, seed=44, device="cuda", fill_device="cuda")
+    q = seeded_q(len(lens), 32, 128, 44, device="cuda")
+    flat = paged_decode_hip(q, c, flat_splits=128).clone()
+    unsplit = paged_decode_hip(q, c, num_splits=1)
+    torch.cuda.synchronize()
+    assert (flat.float() - unsplit.float()).abs().max().item() < ABS_TOL
+    rows = [0, 1, 511, 512, 513, 998, 999]
+    rows = [r for r in rows if lens[r] > 0]
+    want = oracle.reference_decode(q[rows].cpu(), subset_cache(c, rows), out_dtype=torch.float32)
+    assert max_abs(flat[rows], want) < ABS_TOL
+    dead = [b for b, t in enumerate(lens) if t == 0]
+    if dead:
+        assert torch.equal(flat[dead].float().cpu(), torch.zeros((len(dead), 32, 128)))

@@ -360,6 +360,7 @@ def test_flat_splits_for_and_plan_decode():
     assert plan_decode([1024] * FLAT_MERGE_FREE_MAX_BATCH, 8, 4, 256, 1)[2] == 128
     assert plan_decode([1024] * (FLAT_MERGE_FREE_MAX_BATCH + 1), 8, 4, 256, 1)[2] == 0
     assert plan_decode([1024, 1056] * (FLAT_MAX_BATCH // 2 + 1), 8, 4, 256, 1)[2] == 0
+    assert plan_decode([1024, 1056] * (FLAT_MAX_BATCH // 2), 8, 4, 256, 1)[2] == 128
     # with the KV type known, a nearly uniform batch that fills the CUs
     # unsplit stays unsplit while its K/V is small (no merge launch) ...
     assert plan_decode([1024] * 64, 8, 4, 256, 1, kv_dtype="fp16", head_dim=128) == (1, 1024, 0)
