@@ -1284,7 +1284,10 @@ __global__ void __launch_bounds__(kMergeWaves * 64) split_reduce_kernel(const RP
 
   // Few splits (the common case): every lane loads all log2-sum-exps and its
   // slice of every partial in one round trip and folds them in split order.
-  constexpr int kFast = 64 / kPer;
+  // At most 8 held in registers: the merge's VGPRs set how many of its waves
+  // are resident, and 8 measured fastest (C2 3.1 us against 3.9 with 32 at
+  // head_dim 128, 3.4 with 16; 4 sends C3's longer sequences to the slow path).
+  constexpr int kFast = 64 / kPer > 8 ? 8 : 64 / kPer;
   if (S <= kFast) {
     float ls[kFast], v[kFast][kPer];
 #pragma unroll
