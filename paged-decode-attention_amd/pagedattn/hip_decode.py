@@ -29,14 +29,21 @@ from .cache import PagedKVCache
 WAVES_PER_WORKGROUP = 4
 TILE_TOKENS = 32
 SIMDS_PER_CU = 4
-# Workgroups of the decode kernel resident on one CU at head_dim 128 (two
-# 4-wave workgroups: the kernel is built for 2 waves per SIMD).
-RESIDENT_WORKGROUPS_PER_CU = 2
-# Smallest split chunk worth a workgroup (16 tiles, 4 per wave).
-MIN_SPLIT_TOKENS = 512
-# Rounds of resident workgroups a split launch is planned for (measured on
-# the BASELINE ragged / long-context shapes: 2 beats 1 and 3).
-SPLIT_ROUNDS = 2
+# The classic split serves the batches too small for the flat split, which
+# are latency-bound: it is sized for one round of one workgroup per CU, with
+# chunks of at least MIN_SPLIT_TOKENS (2 tiles). Graph-timed whole calls at
+# the Llama-3-8B shape, this rule against the previous one (two rounds of two
+# workgroups per CU, chunks of at least 512 tokens): B = 1, T = 2048 9.6 /
+# 12.3 us; B = 1, T = 8192 13.1 / 14.5; B = 4, T = 512 8.7 / 9.5; B = 4,
+# T = 2048 12.4 / 13.5.
+MIN_SPLIT_TOKENS = 64
+# Sequences this short are never split: the merge launch costs more than the
+# split saves (C1, T <= 192: 4.5 us unsplit, 6.9 with 2-3 splits).
+UNSPLIT_MAX_TOKENS = 256
+# A ragged batch with a workgroup for every CU is split only when its longest
+# sequence exceeds this (B = 32, T <= 512: 11.0 us unsplit, 14.9 with 2
+# splits, 22.6 with 8).
+RAGGED_SPLIT_MIN_TOKENS = 1024
 
 # Flat split: one round of waves, at most FLAT_WAVES_PER_SIMD per SIMD even
 # where the registers allow more. One streaming wave per SIMD measured
@@ -47,6 +54,12 @@ SPLIT_ROUNDS = 2
 # 32-token tiles; smaller batches are latency-bound and run faster unsplit.
 FLAT_WAVES_PER_SIMD = 1
 MIN_FLAT_TILES_PER_WAVE = 4
+# A single sequence up to this length takes the classic split: cut into one
+# chunk per CU it merges 32 partials per head, the flat split 128 (graph-
+# timed whole calls, classic against flat: T = 16384 17.9 / 21.0 us, 32768
+# 27.6 / 30.6, 65536 47.2 / 49.6; at 131072 the flat split wins, 87.9 against
+# 91.4 with 64 splits).
+SINGLE_SEQ_SPLIT_MAX_TOKENS = 65536
 # A nearly uniform batch that fills the CUs unsplit (plan_num_splits gives
 # 1) runs unsplit while its K/V is at most this many bytes: the flat pass
 # streams faster but adds its merge launch (about 4 us). Whole-call
@@ -84,24 +97,30 @@ def pick_num_splits(
     """Split count for the split-KV path, sized for the MI355X's 256 CUs.
 
     Same signature as the reference (triton_decode.py:248-263), MI355X policy
-    from measurements of the BASELINE shapes:
-      * batch*kv_heads >= RESIDENT_WORKGROUPS_PER_CU * CUs (every CU already
-        holds its two resident workgroups): no split; a second pass costs
-        more than the balance it buys on uniform batches;
-      * otherwise enough splits for two rounds of resident workgroups
-        (4 per CU), but never chunks below MIN_SPLIT_TOKENS tokens; no
-        power-of-two rounding and no cap of 64, so a long-context batch of 4
-        uses dozens of splits.
+    from measurements:
+      * batch*kv_heads >= CUs (every CU already has a workgroup) or
+        max_seq_len <= UNSPLIT_MAX_TOKENS: no split;
+      * otherwise enough splits for one workgroup per CU, but never chunks
+        below MIN_SPLIT_TOKENS tokens; no power-of-two rounding and no cap
+        of 64.
     `block_n` is accepted for signature compatibility.
     """
     del block_n
     base = max(1, batch * num_kv_heads)
-    slots = RESIDENT_WORKGROUPS_PER_CU * max(1, sm_count)
-    if base >= slots:
+    if base >= max(1, sm_count) or max_seq_len <= UNSPLIT_MAX_TOKENS:
         return 1
-    want = -(-2 * slots // base)
+    want = -(-max(1, sm_count) // base)
     max_useful = max(1, max_seq_len // MIN_SPLIT_TOKENS)
     return int(max(1, min(want, max_useful, _abi.PA_MAX_SPLITS)))
+
+
+def _fills_unsplit(lens: list[int], num_kv_heads: int, group: int, sm_count: int) -> bool:
+    """A nearly uniform batch (longest <= 1.25 x mean) whose unsplit
+    workgroups already give every CU one."""
+    if not lens or max(lens) == 0:
+        return False
+    units = num_kv_heads * -(-group // _abi.PA_MAX_GROUP)
+    return len(lens) * units >= max(1, sm_count) and max(lens) <= 1.25 * sum(lens) / len(lens)
 
 
 def plan_num_splits(seq_lens, num_kv_heads: int, group: int, sm_count: int) -> tuple[int, int]:
@@ -110,24 +129,36 @@ def plan_num_splits(seq_lens, num_kv_heads: int, group: int, sm_count: int) -> t
     `pick_num_splits` sees only the longest length, so it cannot tell a
     uniform batch (best unsplit when it already fills the CUs) from a ragged
     one (whose long sequences then run alone at the end). With the lengths:
-      * nearly uniform (longest <= 1.25 x mean) and every CU holds its
-        resident workgroups: no split;
-      * otherwise the balanced chunking (every sequence cut with the longest
-        one's chunk) with about SPLIT_ROUNDS rounds of resident workgroups of
-        work: chunk ~ sum(T) * heads / (SPLIT_ROUNDS * slots), at least
-        MIN_SPLIT_TOKENS.
+      * nearly uniform (longest <= 1.25 x mean) with a workgroup for every
+        CU, or no sequence longer than UNSPLIT_MAX_TOKENS: no split;
+      * batches with fewer workgroups than CUs: the balanced chunking (every
+        sequence cut with the longest one's chunk) with one workgroup of
+        work per CU, chunk ~ sum(T) * heads / CUs (twice that for a ragged
+        batch), at least MIN_SPLIT_TOKENS;
+      * ragged batches with a workgroup for every CU: unsplit up to
+        RAGGED_SPLIT_MIN_TOKENS, else about four rounds of workgroups,
+        chunk ~ sum(T) * heads / (4 CUs).
     """
     lens = [max(0, int(t)) for t in seq_lens]
     if not lens or max(lens) == 0:
         return 1, 0
     tmax = max(lens)
-    head_tiles = -(-group // _abi.PA_MAX_GROUP)
-    units = num_kv_heads * head_tiles
-    slots = RESIDENT_WORKGROUPS_PER_CU * max(1, sm_count)
-    mean = sum(lens) / len(lens)
-    if len(lens) * units >= slots and tmax <= 1.25 * mean:
+    units = num_kv_heads * -(-group // _abi.PA_MAX_GROUP)
+    uniform = tmax <= 1.25 * sum(lens) / len(lens)
+    if _fills_unsplit(lens, num_kv_heads, group, sm_count) or tmax <= UNSPLIT_MAX_TOKENS:
         return 1, tmax
-    chunk = max(MIN_SPLIT_TOKENS, sum(lens) * units // (SPLIT_ROUNDS * slots))
+    work, cus = sum(lens) * units, max(1, sm_count)
+    if len(lens) * units >= cus:
+        # every CU has a workgroup already (a ragged batch): split only long
+        # sequences, into several rounds of workgroups
+        if tmax <= RAGGED_SPLIT_MIN_TOKENS:
+            return 1, tmax
+        chunk = work // (4 * cus)
+    else:
+        # one workgroup of work per CU; a ragged batch's chunks twice as long
+        # (its short sequences add partly filled ones)
+        chunk = (1 if uniform else 2) * work // cus
+    chunk = max(MIN_SPLIT_TOKENS, chunk)
     splits = max(1, min(-(-tmax // chunk), _abi.PA_MAX_SPLITS))
     return int(splits), tmax
 
@@ -163,12 +194,14 @@ def plan_decode(seq_lens, num_kv_heads: int, group: int, sm_count: int,
     tiles = sum(-(-t // TILE_TOKENS) for t in lens)
     fits = len(lens) <= FLAT_MAX_BATCH or (len(lens) <= FLAT_MERGE_FREE_MAX_BATCH
                                            and not flat_needs_merge(lens, flat))
+    if len(lens) == 1 and tmax <= SINGLE_SEQ_SPLIT_MAX_TOKENS:
+        fits = False  # the classic split's shorter merge wins
     if fits and tiles >= MIN_FLAT_TILES_PER_WAVE * flat:
         if kv_dtype is not None and head_dim is not None and flat_needs_merge(lens, flat):
             elem = 1 if kv_dtype in ("fp8_e5m2", "int8") else 2
             kv_bytes = sum(lens) * num_kv_heads * head_dim * elem * 2
             if (kv_bytes <= UNSPLIT_MAX_KV_BYTES.get(kv_dtype, 0)
-                    and plan_num_splits(lens, num_kv_heads, group, sm_count)[0] == 1):
+                    and _fills_unsplit(lens, num_kv_heads, group, sm_count)):
                 return 1, tmax, 0
         return 1, tmax, flat
     splits, tmax = plan_num_splits(lens, num_kv_heads, group, sm_count)

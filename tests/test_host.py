@@ -274,8 +274,11 @@ def test_pick_num_splits_policy():
     # enough work already: no split
     assert pick_num_splits(64, 8, 4096, 256) == 1
     assert pick_num_splits(24, 2, 192, 256) == 1  # C1: capped by the short context
-    # long context, tiny batch: hundreds of splits (BASELINE C5 needs >= 256)
-    assert pick_num_splits(4, 8, 131072, 256) >= 16
+    # long context, tiny batch: one workgroup per CU (B * Hkv * S >= CUs)
+    assert pick_num_splits(4, 8, 131072, 256) == 8
+    assert pick_num_splits(1, 8, 131072, 256) == 32
+    assert pick_num_splits(1, 8, 512, 256) == 8      # chunks of at least 64 tokens
+    assert pick_num_splits(32, 8, 4096, 256) == 1    # a workgroup per CU already
     for b, h, t in ((1, 1, 1), (1, 8, 5000), (32, 8, 16384), (4, 8, 131072), (3, 2, 0)):
         s = pick_num_splits(b, h, t, 256)
         assert 1 <= s <= _abi.PA_MAX_SPLITS
@@ -323,9 +326,18 @@ def test_plan_num_splits():
     ragged = torch.exp(math.log(128) + u * (math.log(8192) - math.log(128))).round().long().tolist()
     s, m = plan_num_splits(ragged, 8, 4, 256)
     assert s >= 4 and m == max(ragged)
-    # small batches of long sequences: many splits (BASELINE C5: >= 32)
-    assert plan_num_splits([131072] * 4, 8, 4, 256)[0] >= 32
-    assert plan_num_splits([16384] * 32, 8, 8, 256)[0] >= 4
+    # small batches of long sequences: one chunk of work per CU
+    assert plan_num_splits([131072] * 4, 8, 4, 256) == (8, 131072)
+    assert plan_num_splits([16384] * 32, 8, 8, 256) == (1, 16384)   # 256 units: one per CU
+    assert plan_num_splits([2048], 8, 4, 256) == (32, 2048)           # 64-token chunks
+    # a ragged batch takes chunks twice as long: 2 * 3584 * 8 / 256 = 224 tokens
+    assert plan_num_splits([2048, 1024, 256, 256], 8, 4, 256) == (10, 2048)
+    # a ragged batch with a workgroup per CU: unsplit while its sequences are
+    # short, else about four rounds of workgroups (C3's lengths: 842-token chunks)
+    assert plan_num_splits([500, 20] * 16, 8, 4, 256) == (1, 500)
+    assert s == -(-max(ragged) // (sum(ragged) * 8 // 1024))
+    # short sequences are never split (the merge would cost more)
+    assert plan_num_splits([192, 40, 7], 2, 7, 256) == (1, 192)
     # edge cases
     assert plan_num_splits([], 8, 4, 256) == (1, 0)
     assert plan_num_splits([0, 0], 8, 4, 256) == (1, 0)
@@ -382,8 +394,13 @@ def test_flat_splits_for_and_plan_decode():
     from pagedattn.hip_decode import MIN_FLAT_TILES_PER_WAVE
     f = flat_splits_for(1, 1, 1, 1)
     assert f == 4
-    assert plan_decode([32 * MIN_FLAT_TILES_PER_WAVE * f], 1, 1, 1, 1)[2] == f
-    assert plan_decode([32 * MIN_FLAT_TILES_PER_WAVE * f - 32], 1, 1, 1, 1)[2] == 0
+    half = 16 * MIN_FLAT_TILES_PER_WAVE * f
+    assert plan_decode([half, half], 1, 1, 1, 1)[2] == f
+    assert plan_decode([half, half - 32], 1, 1, 1, 1)[2] == 0
+    # a single sequence takes the classic split up to SINGLE_SEQ_SPLIT_MAX_TOKENS
+    from pagedattn.hip_decode import SINGLE_SEQ_SPLIT_MAX_TOKENS as single
+    assert plan_decode([single], 8, 4, 256, 1)[2] == 0
+    assert plan_decode([single + 32], 8, 4, 256, 1)[2] == 128
 
 
 @cpu_only
