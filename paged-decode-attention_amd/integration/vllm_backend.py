@@ -43,6 +43,7 @@ from pagedattn.config import ModelShape  # noqa: E402
 from pagedattn.hip_decode import (  # noqa: E402
     FLAT_MAX_BATCH,
     MIN_FLAT_TILES_PER_WAVE,
+    SINGLE_SEQ_SPLIT_MAX_TOKENS,
     TILE_TOKENS,
     flat_splits_for,
     flat_waves_per_simd,
@@ -168,7 +169,8 @@ def decode_forward(impl, layer, query, key, value, kv_cache, attn_metadata, outp
     group = impl.num_heads // impl.num_kv_heads
     flat = flat_splits_for(impl.num_kv_heads, group, _cu_count(query.device),
                            flat_waves_per_simd(cache.kv_dtype, impl.head_size))
-    if n <= FLAT_MAX_BATCH and n * -(-msl // TILE_TOKENS) >= MIN_FLAT_TILES_PER_WAVE * flat:
+    single = n == 1 and msl <= SINGLE_SEQ_SPLIT_MAX_TOKENS  # plan_decode's single-sequence rule
+    if not single and n <= FLAT_MAX_BATCH and n * -(-msl // TILE_TOKENS) >= MIN_FLAT_TILES_PER_WAVE * flat:
         decode(query[:n], cache, out=output[:n], sm_scale=impl.scale, flat_splits=flat)
     else:
         splits = pick_num_splits(n, impl.num_kv_heads, msl, _cu_count(query.device))

@@ -206,3 +206,10 @@ def test_decode_forward_takes_the_flat_split_for_large_batches(monkeypatch):
     meta = _meta(max_seq_len=300)
     vb.decode_forward(impl, None, q, q, q, _kv(), meta, torch.zeros_like(q), decode=fake_decode)
     assert calls[-1] == {"num_splits": vb.pick_num_splits(2, 8, 300, 256), "max_seq_len": 300}
+    # so does a single long sequence (its classic merge is shorter than the flat one)
+    meta = _meta(num_actual_tokens=1, max_seq_len=16384,
+                 block_table=torch.zeros((1, 1024), dtype=torch.int32),
+                 seq_lens=torch.full((1,), 16384, dtype=torch.int32))
+    vb.decode_forward(impl, None, q[:1], q[:1], q[:1], _kv(), meta, torch.zeros_like(q[:1]),
+                      decode=fake_decode)
+    assert calls[-1] == {"num_splits": vb.pick_num_splits(1, 8, 16384, 256), "max_seq_len": 16384}
