@@ -44,15 +44,19 @@
 //
 // Quantised KV is dequantised in registers with one v_perm per fp16 pair:
 //   fp8_e5m2 -> fp16: the e5m2 byte is the high byte of the fp16 pattern.
-//   int8 -> fp16 exactly (|x| <= 127): with the byte's sign bit flipped
-//           (one xor per 4 K bytes, per 2 V bytes), b ^ 0x80 = x + 128 is the
-//           mantissa of an fp16 denormal, (x + 128) * 2^-24 (the MFMA keeps
-//           fp16 denormals). The offset is removed after the products, once
-//           per row instead of per element: from each score as
-//           2^-17 * sum(q) of its head, from the output as 2^-17 * sum(P)
-//           of its column (P summed in fp32 by v_dot2); 2^24 is folded into
-//           the scales. The per-(token, head) scale is folded into the
-//           fp32 score (K) and into the probability (V).
+//   int8: with the byte's sign bit flipped (one xor per 4 bytes),
+//         b ^ 0x80 = x + 128 is the mantissa of an fp16 denormal,
+//         (x + 128) * 2^-24, exact (the MFMA and v_fma_mix keep fp16
+//         denormals).
+//     K: the denormals go to the MFMA as they are; the offset leaves each
+//        score once per row, as 2^-17 * sum(q) of its head, and the
+//        per-(token, head) scale times 2^24 multiplies the fp32 score.
+//     V: one v_fma_mix per element forms fp16((x + 128) * 2^-24 * s * 2^24
+//        - 128 * s) = fp16(x * s), the product rounded once to fp32 and
+//        then to fp16 as the reference's dequantised cache holds it, and
+//        P goes to the MFMA in fp16 as for an fp16 cache. (Folding s into
+//        P instead would round s to fp16: a one-token sequence then returns
+//        x * fp16(s), up to 2^-11 relative away from fp16(x * s).)
 
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
@@ -79,10 +83,13 @@ constexpr int kSplitAlign = 32;    // split ranges are multiples of this many to
 constexpr float kRescaleLog2 = 8.0f;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr uint32_t kInt8Sign = 0x80808080u;      // int8 x -> x + 128 in every byte
-constexpr uint32_t kInt8PairSign = 0x00800080u;  // the same for [b, 0, b', 0]
 constexpr float kInt8Unit = 16777216.0f;      // 2^24: int8 operands are (x + 128) * 2^-24
 // s_waitcnt immediate (gfx9 encoding): vmcnt(0), expcnt and lgkmcnt at their maxima
 constexpr int kWaitVmcnt0 = 0x0F70;
+// Buffer resource word 3 for raw (stride 0) byte buffers on gfx9, and the
+// non-temporal cache policy of a buffer load (bit 1 = nt).
+constexpr int kRsrcWord3 = 0x00020000;
+constexpr int kLoadNT = 2;
 // A flat-split wave with at most this many tiles keeps two tiles in flight:
 // short ranges are latency-bound; longer ones stream faster with one.
 constexpr int kDeepTiles = 16;
@@ -202,46 +209,49 @@ __device__ __forceinline__ constexpr uint32_t pair_sel(uint32_t i, uint32_t j) {
 }
 
 // Two stored bytes -> two fp16 bit patterns: one v_perm (int8 sign bits are
-// flipped on the K words before it and on the V pair after it).
+// flipped on the words before it).
 template <int KV>
 __device__ __forceinline__ uint32_t bytes_to_halves(uint32_t hi, uint32_t lo, uint32_t sel) {
   return perm(hi, lo, sel);
 }
 
-// One K/V load. K and V are streamed exactly once per call, so they are
-// fetched with the non-temporal hint.
-template <typename T>
-__device__ __forceinline__ T ldnt(const uint8_t *p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const T *>(p));
+// A raw buffer over the `bytes` bytes from `base` on: a load at a per-lane
+// offset at or past `bytes` returns zeros (the range check of raw buffers).
+// bytes = -1 (2^32 - 1) leaves every offset used here in range.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const uint8_t *base, int bytes = -1) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), (short)0, bytes, kRsrcWord3);
 }
 
+// BYTES from the buffer at voff (per lane) + soff (uniform), non-temporal.
 template <int BYTES>
-__device__ __forceinline__ void load_bytes(uint32_t *w, const uint8_t *p) {
+__device__ __forceinline__ void buf_load_bytes(uint32_t *w, __amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                               uint32_t soff) {
   if constexpr (BYTES == 32) {
-    const u32x4 a = ldnt<u32x4>(p);
-    const u32x4 b = ldnt<u32x4>(p + 16);
+    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kLoadNT);
+    const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, soff, kLoadNT);
     w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
     w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
   } else if constexpr (BYTES == 16) {
-    const u32x4 a = ldnt<u32x4>(p);
+    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kLoadNT);
     w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
   } else if constexpr (BYTES == 8) {
-    const u32x2 a = ldnt<u32x2>(p);
+    const u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, kLoadNT);
     w[0] = a.x; w[1] = a.y;
   } else if constexpr (BYTES == 4) {
-    w[0] = ldnt<uint32_t>(p);
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, kLoadNT);
   } else {
     static_assert(BYTES == 2, "unsupported load width");
-    w[0] = ldnt<uint16_t>(p);
+    w[0] = __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, kLoadNT);
   }
 }
 
+// The bits of one scale (fp16 scales in the low half).
 template <int SC>
-__device__ __forceinline__ float load_scale(const uint8_t *p) {
+__device__ __forceinline__ uint32_t load_scale_bits(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
   if constexpr (SC == PA_SCALE_FP32) {
-    return *reinterpret_cast<const float *>(p);
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0);
   } else {
-    return (float)*reinterpret_cast<const _Float16 *>(p);
+    return __builtin_amdgcn_raw_buffer_load_b16(r, voff, 0, 0);
   }
 }
 
@@ -298,6 +308,37 @@ struct Tile {
   float sc[G::kScales / 64];         // int8: scale j*64 + lane of the tile's (K|V, sub-tile, row)
 };
 
+// The loop-invariant parts of a wave's tile addresses (one kv head): bases
+// at the head, and each lane's byte offsets inside a 16-row sub-tile.
+template <int KV, int D>
+struct TileAddr {
+  const uint8_t *k, *v;    // p.k / p.v + kvh * skh
+  const uint8_t *ks, *vs;  // int8: p.ks / p.vs + kvh * scale bytes
+  uint32_t k_lane;         // row (lane / kKLanesPerRow) % 16; K load i adds row (i * kKRowsPerLoad) % 16
+  uint32_t v_row[4];       // V row load e: row 4c + e % 4, bytes kVBytes * r16 ..
+  uint32_t s_lane;         // int8 scale: row r16
+  uint32_t s_mask[4];      // int8 scale: all ones in lane group lane / 16, else zero
+};
+
+template <int KV, int SC, int D>
+__device__ __forceinline__ TileAddr<KV, D> tile_addr(const KParams &p, int kvh, int lane) {
+  using G = Geo<KV, D>;
+  TileAddr<KV, D> a;
+  const uint32_t skt = (uint32_t)p.skt;
+  a.k = p.k + (int64_t)kvh * p.skh;
+  a.v = p.v + (int64_t)kvh * p.skh;
+  a.ks = p.ks + (int64_t)kvh * (SC == PA_SCALE_FP32 ? 4 : 2);
+  a.vs = p.vs + (int64_t)kvh * (SC == PA_SCALE_FP32 ? 4 : 2);
+  a.k_lane = (uint32_t)((lane / G::kKLanesPerRow) & 15) * skt + 16u * (lane % G::kKLanesPerRow);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    a.v_row[i] = (uint32_t)(4 * (lane >> 4) + i) * skt + (uint32_t)(G::kVBytes * (lane & 15));
+  a.s_lane = (uint32_t)(lane & 15) * (uint32_t)p.sst;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) a.s_mask[g] = (lane >> 4) == g ? ~0u : 0u;
+  return a;
+}
+
 template <int KV, int D>
 struct WaveState {
   using G = Geo<KV, D>;
@@ -306,103 +347,79 @@ struct WaveState {
   float m;                // running max (log2 domain) for head column r16
   float l;                // running sum over this lane's tokens
   // int8 only: 2^-17 * sum(q) of head r16 (the offset in every raw score)
-  // and the sum of this lane's P values (2^-17 times their column sum is
-  // the offset in every output row)
   float qcorr;
-  float wsum;
 };
 
-// int8: take the offsets out of the accumulators,
-// O = (acc - 2^-17 * sum(P)) * 2^24.
-template <int KV, int D>
-__device__ __forceinline__ void remove_offsets(WaveState<KV, D> &st) {
-  using G = Geo<KV, D>;
-  if constexpr (KV == PA_KV_INT8) {
-    const float off = col_sum(st.wsum) * (1.0f / 131072.0f);
-#pragma unroll
-    for (int sl = 0; sl < G::kE; ++sl)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) st.acc[sl][i] = (st.acc[sl][i] - off) * kInt8Unit;
-  }
-}
-
-// Issue the loads of the tile starting at token n0 (< hi). Rows at or past
-// `hi` in the last tile are clamped to valid rows of the sequence: they are
-// read (finite data) and masked out of the softmax by compute_tile.
-// With `wait_prev`, the K/V loads are issued only once the loads issued
-// before them (the tile about to be computed) have arrived: one tile in
-// flight per wave instead of two (the block-table reads still go ahead).
+// Issue the loads of the tile starting at token n0 (< hi). A tile is two
+// 16-row sub-tiles; n0 is a multiple of 32 and pages hold a power of two
+// >= 16 rows, so a sub-tile lies in one page and is read as one raw buffer
+// from its first row. In the last tile, rows at or past `hi` are either
+// read as they are (K rows and K scales: inside the page, finite or not,
+// and their scores are replaced by -inf) or read as zeros through the
+// buffer's range check (V rows and V scales, which the MFMA multiplies by
+// P = 0: zeros keep the products finite). A sub-tile wholly past the end
+// re-reads the last one. With `wait_prev`, the K/V loads are issued only
+// once the loads issued before them (the tile about to be computed) have
+// arrived: one tile in flight per wave instead of two (the block-table
+// reads still go ahead).
 template <int KV, int SC, int D>
-__device__ __forceinline__ void load_tile(Tile<KV, D> &r, const KParams &p, const ro_i32 *bt_row,
-                                          int kvh, int n0, int hi, int lane, bool wait_prev = false) {
+__device__ __forceinline__ void load_tile(Tile<KV, D> &r, const KParams &p, const TileAddr<KV, D> &ta,
+                                          const ro_i32 *bt_row, int n0, int hi, int lane,
+                                          bool wait_prev = false) {
   using G = Geo<KV, D>;
   constexpr int NS = G::kNSub;
-  const int r16 = lane & 15;
-  const int c = lane >> 4;
+  static_assert(NS == 2 && G::kScales == 64, "one scale per lane covers the tile");
+  static_assert(G::kKRowsPerLoad <= 16 || G::kKRowsPerLoad == 32, "K load row layout");
+  const uint32_t skt = (uint32_t)p.skt;
   const int page_mask = (1 << p.log2_page) - 1;
-  const bool tail = n0 + G::kTT > hi;
 
-  int64_t base[NS];
-  int lim[NS];
-  int phys[NS], off[NS];
+  __amdgpu_buffer_rsrc_t rk[NS], rv[NS], rks[NS], rvs[NS];
 #pragma unroll
   for (int u = 0; u < NS; ++u) {
-    // a sub-tile past the end re-reads the last one (a no-op before the tail:
-    // n0 is a multiple of 32 and (hi - 1) & ~15 >= n0 + 16 there)
     const int t0 = min(n0 + 16 * u, (hi - 1) & ~15);
-    phys[u] = min(max(bt_row[t0 >> p.log2_page], 0), p.num_blocks - 1);
-    off[u] = t0 & page_mask;
-    lim[u] = hi - 1 - t0;  // last valid row of the sub-tile (>= 15 unless tail)
-    base[u] = (int64_t)phys[u] * p.skn + (int64_t)off[u] * p.skt + (int64_t)kvh * p.skh;
+    const uint32_t ph = (uint32_t)min(max(bt_row[t0 >> p.log2_page], 0), p.num_blocks - 1);
+    const uint32_t of = (uint32_t)(t0 & page_mask);
+    const int rows = min(hi - t0, 16);  // valid rows of the sub-tile, >= 1
+    const uint64_t row0 = (uint64_t)ph * (uint32_t)p.skn + of * skt;
+    rk[u] = page_rsrc(ta.k + row0);
+    rv[u] = page_rsrc(ta.v + row0, (int)((uint32_t)rows * skt));
+    if constexpr (KV == PA_KV_INT8) {
+      const uint32_t sst = (uint32_t)p.sst;
+      const uint64_t srow0 = (uint64_t)ph * (uint32_t)p.ssn + of * sst;
+      rks[u] = page_rsrc(ta.ks + srow0);
+      rvs[u] = page_rsrc(ta.vs + srow0, (int)((uint32_t)rows * sst));
+    }
   }
-  const uint32_t skt = (uint32_t)p.skt;
   if (wait_prev) __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
 
 #pragma unroll
   for (int i = 0; i < G::kKLoads; ++i) {
-    const int row = i * G::kKRowsPerLoad + lane / G::kKLanesPerRow;  // 0 .. kTT-1
-    // the sub-tile is uniform per instruction unless one instruction spans two
-    const int u = G::kKRowsPerLoad <= 16 ? (i * G::kKRowsPerLoad) >> 4 : row >> 4;
-    int64_t b = base[0];
-    int lm = lim[0];
-#pragma unroll
-    for (int uu = 1; uu < NS; ++uu)
-      if (u == uu) {
-        b = base[uu];
-        lm = lim[uu];
-      }
-    int rr = row & 15;
-    if (tail) rr = min(rr, lm);
-    r.k[i] = ldnt<u32x4>(p.k + b + (uint32_t)rr * skt + 16 * (lane % G::kKLanesPerRow));
-  }
-#pragma unroll
-  for (int e = 0; e < G::kVRows; ++e) {
-    const int u = e >> 2;
-    int rv = 4 * c + (e & 3);
-    if (tail) rv = min(rv, lim[u]);
-    load_bytes<G::kVBytes>(r.v[e], p.v + base[u] + (uint32_t)rv * skt + G::kVBytes * r16);
-  }
-  if constexpr (KV == PA_KV_INT8) {
-    // value j*64 + lane -> (K or V, sub-tile, row): coalesced scale loads
-#pragma unroll
-    for (int j = 0; j < G::kScales / 64; ++j) {
-      const int vi = j * 64 + lane;
-      const int which = vi / (16 * NS);
-      const int u = (vi >> 4) % NS;
-      int ph = phys[0], of = off[0], lm = lim[0];
-#pragma unroll
-      for (int uu = 1; uu < NS; ++uu)
-        if (u == uu) {
-          ph = phys[uu];
-          of = off[uu];
-          lm = lim[uu];
-        }
-      const int row = tail ? min(r16, lm) : r16;
-      const uint8_t *sp = which ? p.vs : p.ks;
-      const int64_t so = (int64_t)ph * p.ssn + (int64_t)(of + row) * p.sst +
-                         (int64_t)kvh * (SC == PA_SCALE_FP32 ? 4 : 2);
-      r.sc[j] = load_scale<SC>(sp + so);
+    if constexpr (G::kKRowsPerLoad <= 16) {
+      // the load's rows lie in sub-tile (i * rows) / 16
+      const int u = (i * G::kKRowsPerLoad) >> 4;
+      const uint32_t soff = (uint32_t)((i * G::kKRowsPerLoad) & 15) * skt;
+      r.k[i] = __builtin_amdgcn_raw_buffer_load_b128(rk[u], ta.k_lane, soff, kLoadNT);
+    } else {
+      // 32 rows per load: lanes 0-31 hold sub-tile 0, lanes 32-63 sub-tile 1;
+      // every lane reads its row of both sub-tiles and keeps its own
+      const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rk[0], ta.k_lane, 0, kLoadNT);
+      const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(rk[1], ta.k_lane, 0, kLoadNT);
+      r.k[i] = lane < 32 ? a : b;
     }
+  }
+#pragma unroll
+  for (int e = 0; e < G::kVRows; ++e) buf_load_bytes<G::kVBytes>(r.v[e], rv[e >> 2], ta.v_row[e & 3], 0);
+  if constexpr (KV == PA_KV_INT8) {
+    // lane group g = lane / 16 holds scale (K | V)[g / 2] of sub-tile g % 2:
+    // four loads, each with a uniform buffer, combined by bit masks (a
+    // select between the loads would become one load from a per-lane buffer)
+    const uint32_t k0 = load_scale_bits<SC>(rks[0], ta.s_lane);
+    const uint32_t k1 = load_scale_bits<SC>(rks[1], ta.s_lane);
+    const uint32_t v0 = load_scale_bits<SC>(rvs[0], ta.s_lane);
+    const uint32_t v1 = load_scale_bits<SC>(rvs[1], ta.s_lane);
+    const uint32_t bits = (k0 & ta.s_mask[0]) | (k1 & ta.s_mask[1]) | (v0 & ta.s_mask[2]) | (v1 & ta.s_mask[3]);
+    r.sc[0] = SC == PA_SCALE_FP32 ? __builtin_bit_cast(float, bits)
+                                  : (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
   }
 }
 
@@ -431,8 +448,12 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
   // back those of its tokens {16u + 4c + i} where they are used (K after the
   // QK products, V for the P operand), so none are live across the MFMAs ----
   if constexpr (KV == PA_KV_INT8) {
+    // (entries 0 .. kTT-1 are K scales, stored times qk_scale * 2^24, the
+    // rest V scales, stored times 2^24)
+    const float k_unit = p.qk_scale * kInt8Unit;
 #pragma unroll
-    for (int j = 0; j < G::kScales / 64; ++j) sc_lds[j * 64 + lane] = r.sc[j];
+    for (int j = 0; j < G::kScales / 64; ++j)
+      sc_lds[j * 64 + lane] = r.sc[j] * ((j * 64 + lane >= G::kTT) ? kInt8Unit : k_unit);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -477,12 +498,11 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
   // ---- online softmax over the tokens this lane holds for head r16 ----
   float s[NV];
   if constexpr (KV == PA_KV_INT8) {
-    const float unit_scale = p.qk_scale * kInt8Unit;
 #pragma unroll
     for (int u = 0; u < NS; ++u) {
       const f32x4 kq = *reinterpret_cast<const f32x4 *>(sc_lds + 16 * u + 4 * c);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) s[4 * u + i] = sacc[u][i] * (kq[i] * unit_scale);
+      for (int i = 0; i < 4; ++i) s[4 * u + i] = sacc[u][i] * kq[i];
     }
   } else {
 #pragma unroll
@@ -507,7 +527,6 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
     st.l *= alpha;
 #pragma unroll
     for (int sl = 0; sl < G::kE; ++sl) st.acc[sl] *= alpha;
-    if constexpr (KV == PA_KV_INT8) st.wsum *= alpha;
     st.m = m_new;
   }
 
@@ -523,18 +542,8 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
 #pragma unroll
   for (int pp = 0; pp < NS / 2; ++pp) {
     f16x8 pop;
-    if constexpr (KV == PA_KV_INT8) {
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        const int u = 2 * pp + h2;
-        const f32x4 vq = *reinterpret_cast<const f32x4 *>(sc_lds + 16 * (NS + u) + 4 * c);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) pop[4 * h2 + i] = (_Float16)(pr[4 * u + i] * vq[i]);
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) pop[e] = (_Float16)pr[8 * pp + e];
-    }
+    for (int e = 0; e < 8; ++e) pop[e] = (_Float16)pr[8 * pp + e];
     if constexpr (G::kElem == 2) {
 #pragma unroll
       for (int sl = 0; sl < G::kE; ++sl) {
@@ -550,9 +559,28 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
         st.acc[sl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop, st.acc[sl], 0, 0, 0);
       }
     } else {
+      // int8: element e of the lane's operand is token 16 * (2pp + e / 4)
+      // + 4c + e % 4, with V scale vs[e] = s * 2^24 and vc[e] = -128 * s
+      float vs[8], vc[8];
+      if constexpr (KV == PA_KV_INT8) {
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          const f32x4 vq = *reinterpret_cast<const f32x4 *>(sc_lds + 16 * (NS + 2 * pp + h2) + 4 * c);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            vs[4 * h2 + i] = vq[i];
+            vc[4 * h2 + i] = vq[i] * (-1.0f / 131072.0f);
+          }
+        }
+      }
       // word wi of a row holds head-dim elements 4*wi .. 4*wi+3 of the lane's
-      // slab group (int8: the pair's sign bits are flipped after the perm,
-      // which keeps the tile registers as loaded)
+      // slab group (int8: sign bits flipped once per word)
+      uint32_t vw[8][G::kVWords];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int w = 0; w < G::kVWords; ++w)
+          vw[e][w] = (KV == PA_KV_INT8) ? (r.v[8 * pp + e][w] ^ kInt8Sign) : r.v[8 * pp + e][w];
 #pragma unroll
       for (int sl = 0; sl < G::kE; ++sl) {
         const int wi = sl >> 2;
@@ -560,21 +588,16 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
         uint32_t h[4];
 #pragma unroll
         for (int m2 = 0; m2 < 4; ++m2) {
-          h[m2] = bytes_to_halves<KV>(r.v[8 * pp + 2 * m2 + 1][wi], r.v[8 * pp + 2 * m2][wi],
-                                      pair_sel<KV>(b, b));
-          if constexpr (KV == PA_KV_INT8) h[m2] ^= kInt8PairSign;
+          h[m2] = bytes_to_halves<KV>(vw[2 * m2 + 1][wi], vw[2 * m2][wi], pair_sel<KV>(b, b));
+          if constexpr (KV == PA_KV_INT8) {
+            const f16x2 u2 = __builtin_bit_cast(f16x2, h[m2]);
+            const f16x2 x2 = {(_Float16)__builtin_fmaf((float)u2[0], vs[2 * m2], vc[2 * m2]),
+                              (_Float16)__builtin_fmaf((float)u2[1], vs[2 * m2 + 1], vc[2 * m2 + 1])};
+            h[m2] = __builtin_bit_cast(uint32_t, x2);
+          }
         }
         const f16x8 vop = as_f16x8(h[0], h[1], h[2], h[3]);
         st.acc[sl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop, st.acc[sl], 0, 0, 0);
-      }
-    }
-    if constexpr (KV == PA_KV_INT8) {
-      // sum(P) of this lane's tokens, exactly the P the MFMAs saw
-      const f16x2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
-#pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        const f16x2 pp2 = {pop[e], pop[e + 1]};
-        st.wsum = __builtin_amdgcn_fdot2(pp2, one2, st.wsum, false);
       }
     }
   }
@@ -621,7 +644,6 @@ __device__ __forceinline__ void reset_state(WaveState<KV, D> &st) {
   st.l = 0.f;
 #pragma unroll
   for (int sl = 0; sl < G::kE; ++sl) st.acc[sl] = f32x4{0.f, 0.f, 0.f, 0.f};
-  st.wsum = 0.f;
 }
 
 // One lane's share of a finished row of head h: y[0 .. 4*kE) = O[h][d0 ..)
@@ -825,6 +847,7 @@ paged_decode_kernel(const KParams p) {
   load_q(st, p, b, qh0, nh, r16, c);
 
   const ro_i32 *bt_row = ro(p.bt) + (int64_t)b * p.sbtb;
+  const TileAddr<KV, D> addr = tile_addr<KV, SC, D>(p, kvh, lane);
   float *sc_lds = sm_sc[wave];
   uint8_t *k_lds = sm_raw + wave * G::kKSlotBytes;
   const int ntiles = (hi > lo) ? (hi - lo + G::kTT - 1) / G::kTT : 0;
@@ -834,16 +857,16 @@ paged_decode_kernel(const KParams p) {
   if (cnt > 0) {
     if constexpr (G::kPrefetch) {
       Tile<KV, D> ta, tb;
-      load_tile<KV, SC, D>(ta, p, bt_row, kvh, n0_of(0), hi, lane);
+      load_tile<KV, SC, D>(ta, p, addr, bt_row, n0_of(0), hi, lane);
       int i = 0;
       for (; i + 2 < cnt; i += 2) {
-        load_tile<KV, SC, D>(tb, p, bt_row, kvh, n0_of(i + 1), hi, lane);
+        load_tile<KV, SC, D>(tb, p, addr, bt_row, n0_of(i + 1), hi, lane);
         compute_tile<KV, SC, D>(st, ta, p, n0_of(i), hi, lane, sc_lds, k_lds);
-        load_tile<KV, SC, D>(ta, p, bt_row, kvh, n0_of(i + 2), hi, lane);
+        load_tile<KV, SC, D>(ta, p, addr, bt_row, n0_of(i + 2), hi, lane);
         compute_tile<KV, SC, D>(st, tb, p, n0_of(i + 1), hi, lane, sc_lds, k_lds);
       }
       if (i + 1 < cnt) {
-        load_tile<KV, SC, D>(tb, p, bt_row, kvh, n0_of(i + 1), hi, lane);
+        load_tile<KV, SC, D>(tb, p, addr, bt_row, n0_of(i + 1), hi, lane);
         compute_tile<KV, SC, D>(st, ta, p, n0_of(i), hi, lane, sc_lds, k_lds);
         compute_tile<KV, SC, D>(st, tb, p, n0_of(i + 1), hi, lane, sc_lds, k_lds);
       } else {
@@ -852,13 +875,11 @@ paged_decode_kernel(const KParams p) {
     } else {
       for (int i = 0; i < cnt; ++i) {
         Tile<KV, D> t;
-        load_tile<KV, SC, D>(t, p, bt_row, kvh, n0_of(i), hi, lane);
+        load_tile<KV, SC, D>(t, p, addr, bt_row, n0_of(i), hi, lane);
         compute_tile<KV, SC, D>(st, t, p, n0_of(i), hi, lane, sc_lds, k_lds);
       }
     }
   }
-
-  remove_offsets(st);
 
   // ---- merge the waves through LDS ----
   const float lw = col_sum(st.l);
@@ -1117,6 +1138,7 @@ paged_decode_flat_kernel(const KParams p) {
 
   float *sc_lds = sm_sc[wave];
   uint8_t *k_lds = sm_k + wave * G::kKSlotBytes;
+  const TileAddr<KV, D> addr = tile_addr<KV, SC, D>(p, kvh, lane);
 
   auto bt_of = [&](int b) { return ro(p.bt) + (int64_t)b * p.sbtb; };
   // After computing the wave's i-th tile: close the segment at a sequence
@@ -1124,7 +1146,6 @@ paged_decode_flat_kernel(const KParams p) {
   auto post = [&](int i) {
     const bool seq_end = cc.t + 1 == cc.tiles;
     if (seq_end || i + 1 == n) {
-      remove_offsets(st);
       const float L = col_sum(st.l);
       const float inv = (L > 0.f) ? 1.0f / L : 0.f;
       if (r16 < nh) {
@@ -1147,21 +1168,21 @@ paged_decode_flat_kernel(const KParams p) {
   if constexpr (G::kPrefetch) {
     const bool shallow = n > kDeepTiles;
     Tile<KV, D> ta, tb;
-    load_tile<KV, SC, D>(ta, p, bt_of(lc.b), kvh, n0_of(lc), lc.len, lane);
+    load_tile<KV, SC, D>(ta, p, addr, bt_of(lc.b), n0_of(lc), lc.len, lane);
     int i = 0;
     for (; i + 2 < n; i += 2) {
       cursor_next(lc, ro(p.seq_lens), p.batch, p.max_tokens);
-      load_tile<KV, SC, D>(tb, p, bt_of(lc.b), kvh, n0_of(lc), lc.len, lane, shallow);
+      load_tile<KV, SC, D>(tb, p, addr, bt_of(lc.b), n0_of(lc), lc.len, lane, shallow);
       compute_tile<KV, SC, D>(st, ta, p, n0_of(cc), cc.len, lane, sc_lds, k_lds);
       post(i);
       cursor_next(lc, ro(p.seq_lens), p.batch, p.max_tokens);
-      load_tile<KV, SC, D>(ta, p, bt_of(lc.b), kvh, n0_of(lc), lc.len, lane, shallow);
+      load_tile<KV, SC, D>(ta, p, addr, bt_of(lc.b), n0_of(lc), lc.len, lane, shallow);
       compute_tile<KV, SC, D>(st, tb, p, n0_of(cc), cc.len, lane, sc_lds, k_lds);
       post(i + 1);
     }
     if (i + 1 < n) {
       cursor_next(lc, ro(p.seq_lens), p.batch, p.max_tokens);
-      load_tile<KV, SC, D>(tb, p, bt_of(lc.b), kvh, n0_of(lc), lc.len, lane, shallow);
+      load_tile<KV, SC, D>(tb, p, addr, bt_of(lc.b), n0_of(lc), lc.len, lane, shallow);
       compute_tile<KV, SC, D>(st, ta, p, n0_of(cc), cc.len, lane, sc_lds, k_lds);
       post(i);
       compute_tile<KV, SC, D>(st, tb, p, n0_of(cc), cc.len, lane, sc_lds, k_lds);
@@ -1173,7 +1194,7 @@ paged_decode_flat_kernel(const KParams p) {
   } else {
     for (int i = 0; i < n; ++i) {
       Tile<KV, D> t;
-      load_tile<KV, SC, D>(t, p, bt_of(cc.b), kvh, n0_of(cc), cc.len, lane);
+      load_tile<KV, SC, D>(t, p, addr, bt_of(cc.b), n0_of(cc), cc.len, lane);
       compute_tile<KV, SC, D>(st, t, p, n0_of(cc), cc.len, lane, sc_lds, k_lds);
       post(i);
     }
@@ -1429,6 +1450,8 @@ int build_params(const pa_decode_args *a, bool need_partials, KParams *kp) {
     if (a->stride_sn < 0 || a->stride_st < 0)
       return fail(PA_ERR_INVALID, "scale strides must be non-negative");
     const int sb = a->scale_dtype == PA_SCALE_FP32 ? 4 : 2;
+    if (a->stride_sn * sb >= (int64_t(1) << 32) || (int64_t)a->block_size * a->stride_st * sb >= (int64_t(1) << 31))
+      return fail(PA_ERR_UNSUPPORTED, "scale page stride exceeds 4 GiB or a scale page 2 GiB");
     if (!aligned(a->k_scale, sb) || !aligned(a->v_scale, sb))
       return fail(PA_ERR_INVALID, "scale pointers must be %d-byte aligned", sb);
   } else if (a->scale_dtype != PA_SCALE_NONE) {
@@ -1452,9 +1475,13 @@ int build_params(const pa_decode_args *a, bool need_partials, KParams *kp) {
   if (!aligned(a->k_cache, 16) || !aligned(a->v_cache, 16) || (a->stride_kn * elem) % 16 ||
       (a->stride_kt * elem) % 16 || (a->stride_kh * elem) % 16)
     return fail(PA_ERR_INVALID, "k_cache/v_cache and their strides must be 16-byte aligned");
-  // in-page row offsets are 32-bit in the kernel
+  // in-page row offsets are 32-bit in the kernel, and so are the page
+  // strides that a block index multiplies
   if ((int64_t)a->block_size * a->stride_kt * elem >= (int64_t(1) << 31))
     return fail(PA_ERR_UNSUPPORTED, "page of %d tokens spans more than 2 GiB", a->block_size);
+  if (a->stride_kn * elem >= (int64_t(1) << 32))
+    return fail(PA_ERR_UNSUPPORTED, "page stride of %lld bytes exceeds 4 GiB",
+                (long long)(a->stride_kn * elem));
   if (need_partials) {
     if (a->stride_pb < 0 || a->stride_ph < 0 || a->stride_ps < 0 || a->stride_lb < 0 ||
         a->stride_lh < 0)

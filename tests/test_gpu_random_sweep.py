@@ -53,6 +53,13 @@ def test_random_case(case):
     run_case(1000 + case)
 
 
+# Draws that once failed: 10259 (int8 with fp32 scales, a ragged batch with
+# one-token sequences, where an fp16-rounded V scale cost 2.3e-3).
+@pytest.mark.parametrize("case", [10259])
+def test_random_regression_case(case):
+    run_case(case)
+
+
 def run_case(case):
     hq, hkv, d, kv, sdt, page, lens, io, mode, knob = _draw(case)
     print(f"case {case}: hq={hq} hkv={hkv} d={d} kv={kv} scales={sdt} page={page} "
