@@ -44,18 +44,20 @@
 //
 // Quantised KV is dequantised in registers with one v_perm per fp16 pair:
 //   fp8_e5m2 -> fp16: the e5m2 byte is the high byte of the fp16 pattern.
-//   int8: with the byte's sign bit flipped (one xor per 4 bytes),
-//         b ^ 0x80 = x + 128 is the mantissa of an fp16 denormal,
-//         (x + 128) * 2^-24, exact (the MFMA and v_fma_mix keep fp16
-//         denormals).
-//     K: the denormals go to the MFMA as they are; the offset leaves each
-//        score once per row, as 2^-17 * sum(q) of its head, and the
-//        per-(token, head) scale times 2^24 multiplies the fp32 score.
-//     V: one v_fma_mix per element forms fp16((x + 128) * 2^-24 * s * 2^24
-//        - 128 * s) = fp16(x * s), the product rounded once to fp32 and
-//        then to fp16 as the reference's dequantised cache holds it, and
-//        P goes to the MFMA in fp16 as for an fp16 cache. (Folding s into
-//        P instead would round s to fp16: a one-token sequence then returns
+//   int8 K: no dequant. Q is held per head as 16-bit fixed point,
+//        round(q * 2^e) = 256 * hi + lo with hi, lo in int8, and two
+//        v_mfma_i32_16x16x64_i8 per 64 head dims give the integer score
+//        256 * (K.hi) + K.lo exactly; 2^-e times the per-(token, head) scale
+//        times qk_scale makes it the fp32 score. The fixed point moves each
+//        q element by at most 2^-14 of its head's max|q|.
+//   int8 V: with the byte's sign bit flipped (one xor per 4 bytes),
+//        b ^ 0x80 = x + 128 is the mantissa of an fp16 denormal,
+//        (x + 128) * 2^-24, exact (v_fma_mix keeps fp16 denormals); one
+//        v_fma_mix per element forms fp16((x + 128) * 2^-24 * s * 2^24
+//        - 128 * s) = fp16(x * s), the product rounded once to fp32 and then
+//        to fp16 as the reference's dequantised cache holds it, and P goes to
+//        the MFMA in fp16 as for an fp16 cache. (Folding s into P instead
+//        would round s to fp16: a one-token sequence then returns
 //        x * fp16(s), up to 2^-11 relative away from fp16(x * s).)
 
 #include <hip/hip_runtime.h>
@@ -76,6 +78,7 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 4;          // waves per workgroup (unsplit / classic split)
 constexpr int kFlatWaves = 4;      // flat kernel: one wave per SIMD of a CU
@@ -83,7 +86,7 @@ constexpr int kSplitAlign = 32;    // split ranges are multiples of this many to
 constexpr float kRescaleLog2 = 8.0f;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr uint32_t kInt8Sign = 0x80808080u;      // int8 x -> x + 128 in every byte
-constexpr float kInt8Unit = 16777216.0f;      // 2^24: int8 operands are (x + 128) * 2^-24
+constexpr float kInt8Unit = 16777216.0f;      // 2^24: int8 V operands are (x + 128) * 2^-24
 // s_waitcnt immediate (gfx9 encoding): vmcnt(0), expcnt and lgkmcnt at their maxima
 constexpr int kWaitVmcnt0 = 0x0F70;
 // Buffer resource word 3 for raw (stride 0) byte buffers on gfx9, and the
@@ -157,6 +160,21 @@ __device__ __forceinline__ float col_sum(float x) {
 // (codes 0-3 pick `lo`, 4-7 pick `hi`, 0x0c gives 0x00).
 __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
   return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+// Per-half unsigned 16-bit maximum of two packed pairs.
+__device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
+  typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+  const u16x2 x = __builtin_bit_cast(u16x2, a), y = __builtin_bit_cast(u16x2, b);
+  return __builtin_bit_cast(uint32_t, u16x2{x[0] > y[0] ? x[0] : y[0], x[1] > y[1] ? x[1] : y[1]});
+}
+
+// floor(x) as int32 in one instruction (the compiler keeps floor and the
+// conversion apart).
+__device__ __forceinline__ int cvt_flr_i32(float x) {
+  int r;
+  asm("v_cvt_flr_i32_f32 %0, %1" : "=v"(r) : "v"(x));
+  return r;
 }
 
 __device__ __forceinline__ f16x8 as_f16x8(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
@@ -275,7 +293,8 @@ __device__ __forceinline__ const ro_i32 *ro(const int32_t *ptr) { return (const 
 template <int KV, int D>
 struct Geo {
   static constexpr int kElem = (KV == PA_KV_FP16 || KV == PA_KV_BF16) ? 2 : 1;  // stored bytes/elem
-  static constexpr int kKSteps = D / 32;                    // QK MFMAs per sub-tile
+  static constexpr int kKSteps = D / 32;                    // QK MFMAs per sub-tile (fp16 operands)
+  static constexpr int kQBlocks = (D + 63) / 64;            // int8: 64-wide QK blocks
   static constexpr int kE = D / 16;                         // V elems per lane row
   static constexpr int kVBytes = kE * kElem;                // V bytes per lane row
   static constexpr int kVWords = (kVBytes + 3) / 4;
@@ -346,8 +365,12 @@ struct WaveState {
   f32x4 acc[G::kE];       // O^T accumulators, one 16x16 block per d-slab
   float m;                // running max (log2 domain) for head column r16
   float l;                // running sum over this lane's tokens
-  // int8 only: 2^-17 * sum(q) of head r16 (the offset in every raw score)
-  float qcorr;
+  // int8 only: head r16's q as 16-bit fixed point, round(q * 2^e) = 256 * hi
+  // + lo with hi, lo in int8, as i8 MFMA B-operands (lane c holds head dims
+  // 64 * blk + 16c .. +15), and qinv = 2^-e
+  i32x4 qhi[G::kQBlocks];
+  i32x4 qlo[G::kQBlocks];
+  float qinv;
 };
 
 // Issue the loads of the tile starting at token n0 (< hi). A tile is two
@@ -448,46 +471,53 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
   // back those of its tokens {16u + 4c + i} where they are used (K after the
   // QK products, V for the P operand), so none are live across the MFMAs ----
   if constexpr (KV == PA_KV_INT8) {
-    // (entries 0 .. kTT-1 are K scales, stored times qk_scale * 2^24, the
-    // rest V scales, stored times 2^24)
-    const float k_unit = p.qk_scale * kInt8Unit;
+    // (entries 0 .. kTT-1 are K scales, stored times qk_scale, the rest V
+    // scales, stored times 2^24)
 #pragma unroll
     for (int j = 0; j < G::kScales / 64; ++j)
-      sc_lds[j * 64 + lane] = r.sc[j] * ((j * 64 + lane >= G::kTT) ? kInt8Unit : k_unit);
+      sc_lds[j * 64 + lane] = r.sc[j] * ((j * 64 + lane >= G::kTT) ? kInt8Unit : p.qk_scale);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 
-  // ---- S^T = K Q^T, one 16-token sub-tile at a time (int8: the
-  // accumulator starts at -2^-17 * sum(q), the operands' offset) ----
+  // ---- S^T = K Q^T, one 16-token sub-tile at a time ----
   f32x4 sacc[NS];
 #pragma unroll
   for (int u = 0; u < NS; ++u) {
     f32x4 a = {0.f, 0.f, 0.f, 0.f};
-    if constexpr (KV == PA_KV_INT8) a = f32x4{-st.qcorr, -st.qcorr, -st.qcorr, -st.qcorr};
+    if constexpr (KV == PA_KV_INT8) {
+      // int8 K bytes straight from LDS against Q's two int8 halves: the
+      // integer score 256 * (K.hi) + K.lo is exact in int32
+      i32x4 ahi = {0, 0, 0, 0}, alo = {0, 0, 0, 0};
 #pragma unroll
-    for (int ks = 0; ks < G::kKSteps; ++ks) {
-      f16x8 kop;
-      const uint8_t *src = k_lds + (16 * u + r16) * G::kKSlotStride + (32 * ks + 8 * c) * G::kElem;
-      if constexpr (KV == PA_KV_BF16) {
-        kop = bf16x8_to_f16x8(*reinterpret_cast<const u32x4 *>(src));
-      } else if constexpr (G::kElem == 2) {
-        kop = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4 *>(src));
-      } else {
-        const u32x2 w = *reinterpret_cast<const u32x2 *>(src);
-        uint32_t w0 = w.x;
-        uint32_t w1 = w.y;
-        if constexpr (KV == PA_KV_INT8) {
-          w0 ^= kInt8Sign;
-          w1 ^= kInt8Sign;
-        }
-        kop = as_f16x8(bytes_to_halves<KV>(w0, w0, pair_sel<KV>(0, 1)),
-                       bytes_to_halves<KV>(w0, w0, pair_sel<KV>(2, 3)),
-                       bytes_to_halves<KV>(w1, w1, pair_sel<KV>(0, 1)),
-                       bytes_to_halves<KV>(w1, w1, pair_sel<KV>(2, 3)));
+      for (int kb = 0; kb < G::kQBlocks; ++kb) {
+        // head_dim 32: lanes c >= 2 have zero Q and read a valid row piece
+        const int col = D >= 64 ? 64 * kb + 16 * c : 16 * (c & 1);
+        const i32x4 kop = *reinterpret_cast<const i32x4 *>(k_lds + (16 * u + r16) * G::kKSlotStride + col);
+        ahi = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop, st.qhi[kb], ahi, 0, 0, 0);
+        alo = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop, st.qlo[kb], alo, 0, 0, 0);
       }
-      a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, st.qop[ks], a, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = (float)((ahi[i] << 8) + alo[i]);
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < G::kKSteps; ++ks) {
+        f16x8 kop;
+        const uint8_t *src = k_lds + (16 * u + r16) * G::kKSlotStride + (32 * ks + 8 * c) * G::kElem;
+        if constexpr (KV == PA_KV_BF16) {
+          kop = bf16x8_to_f16x8(*reinterpret_cast<const u32x4 *>(src));
+        } else if constexpr (G::kElem == 2) {
+          kop = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4 *>(src));
+        } else {
+          const u32x2 w = *reinterpret_cast<const u32x2 *>(src);
+          kop = as_f16x8(bytes_to_halves<KV>(w.x, w.x, pair_sel<KV>(0, 1)),
+                         bytes_to_halves<KV>(w.x, w.x, pair_sel<KV>(2, 3)),
+                         bytes_to_halves<KV>(w.y, w.y, pair_sel<KV>(0, 1)),
+                         bytes_to_halves<KV>(w.y, w.y, pair_sel<KV>(2, 3)));
+        }
+        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, st.qop[ks], a, 0, 0, 0);
+      }
     }
     sacc[u] = a;
   }
@@ -502,7 +532,7 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
     for (int u = 0; u < NS; ++u) {
       const f32x4 kq = *reinterpret_cast<const f32x4 *>(sc_lds + 16 * u + 4 * c);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) s[4 * u + i] = sacc[u][i] * kq[i];
+      for (int i = 0; i < 4; ++i) s[4 * u + i] = sacc[u][i] * (kq[i] * st.qinv);
     }
   } else {
 #pragma unroll
@@ -617,23 +647,63 @@ __device__ __forceinline__ void load_q(WaveState<KV, D> &st, const KParams &p, i
   const bool hv = r16 < nh;
   const uint16_t *qrow = reinterpret_cast<const uint16_t *>(p.q) + (int64_t)b * p.sqb +
                          (int64_t)(qh0 + (hv ? r16 : 0)) * p.sqh;
-#pragma unroll
-  for (int ks = 0; ks < G::kKSteps; ++ks) {
+  // 8 q values from head dim d0 on, as fp16 (bf16 rounded to fp16 first,
+  // the reference's q.to(fp16)); zeros for padded heads
+  auto q8 = [&](int d0) {
     f16x8 qv = {0, 0, 0, 0, 0, 0, 0, 0};
     if (hv) {
-      const u32x4 w = *reinterpret_cast<const u32x4 *>(qrow + 32 * ks + 8 * c);
+      const u32x4 w = *reinterpret_cast<const u32x4 *>(qrow + d0);
       qv = p.io_bf16 ? bf16x8_to_f16x8(w) : __builtin_bit_cast(f16x8, w);
     }
-    st.qop[ks] = qv;
-  }
-  if constexpr (KV == PA_KV_INT8) {
-    // 2^-17 * sum over head_dim of this head's q (lane c holds 8 of every 32)
-    float qs = 0.f;
+    return qv;
+  };
+  if constexpr (KV != PA_KV_INT8) {
 #pragma unroll
-    for (int ks = 0; ks < G::kKSteps; ++ks)
+    for (int ks = 0; ks < G::kKSteps; ++ks) st.qop[ks] = q8(32 * ks + 8 * c);
+  } else {
+    // lane c holds head dims 64 * blk + 16c .. +15 (head_dim 32: lanes c < 2).
+    // max|q| on the fp16 bit patterns: with the sign cleared they order as
+    // the values do, two per v_pk_max_u16
+    constexpr int NB = G::kQBlocks;
+    f16x8 qh[NB][2];
+    uint32_t mx = 0;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) qs += (float)st.qop[ks][e];
-    st.qcorr = col_sum(qs) * (1.0f / 131072.0f);
+    for (int kb = 0; kb < NB; ++kb) {
+      const int d0 = 64 * kb + 16 * c;
+      const bool live = D >= 64 || c < 2;
+#pragma unroll
+      for (int hlf = 0; hlf < 2; ++hlf) {
+        qh[kb][hlf] = live ? q8(d0 + 8 * hlf) : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        const u32x4 w = __builtin_bit_cast(u32x4, qh[kb][hlf]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mx = pk_max_u16(mx, w[i] & 0x7fff7fffu);
+      }
+    }
+    float amax = (float)__builtin_bit_cast(_Float16, (uint16_t)max(mx & 0xffffu, mx >> 16));
+    amax = col_max(amax);
+    // amax in [2^(x-1), 2^x): scaled by 2^(14 - x) it is below 2^14, so
+    // |Q| = |round(q * 2^e)| <= 2^14 and hi = (Q + 128) >> 8 stays within
+    // +-64, lo = Q - 256 hi within -128 .. 127. With t = Q + 128 (one fma
+    // and a floor: round half up), hi is byte 1 of t and lo byte 0 of t
+    // with its top bit flipped.
+    const int e = amax > 0.f ? 14 - __builtin_amdgcn_frexp_expf(amax) : 0;
+    st.qinv = __builtin_ldexpf(1.0f, -e);
+    const float sc = __builtin_ldexpf(1.0f, e);
+#pragma unroll
+    for (int kb = 0; kb < NB; ++kb) {
+      uint32_t hw[4], lw[4];
+#pragma unroll
+      for (int w4 = 0; w4 < 4; ++w4) {
+        uint32_t t[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          t[j] = (uint32_t)cvt_flr_i32(__builtin_fmaf((float)qh[kb][w4 >> 1][4 * (w4 & 1) + j], sc, 128.5f));
+        hw[w4] = perm(t[1], t[0], 0x0c0c0501u) | perm(t[3], t[2], 0x05010c0cu);
+        lw[w4] = (perm(t[1], t[0], 0x0c0c0400u) | perm(t[3], t[2], 0x04000c0cu)) ^ kInt8Sign;
+      }
+      st.qhi[kb] = i32x4{(int)hw[0], (int)hw[1], (int)hw[2], (int)hw[3]};
+      st.qlo[kb] = i32x4{(int)lw[0], (int)lw[1], (int)lw[2], (int)lw[3]};
+    }
   }
 }
 
