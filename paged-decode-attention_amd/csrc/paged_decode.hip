@@ -1236,7 +1236,9 @@ paged_decode_flat_kernel(const KParams p) {
   auto n0_of = [](const SeqCursor &cur) { return cur.t * G::kTT; };
 
   if constexpr (G::kPrefetch) {
-    const bool shallow = n > kDeepTiles;
+    // tiles of rows up to 64 bytes (4 KB) keep two in flight at any length:
+    // one in flight per wave leaves too few bytes in flight for HBM
+    const bool shallow = G::kRowBytes > 64 && n > kDeepTiles;
     Tile<KV, D> ta, tb;
     load_tile<KV, SC, D>(ta, p, addr, bt_of(lc.b), n0_of(lc), lc.len, lane);
     int i = 0;
