@@ -37,6 +37,13 @@
  *   part_lse   [batch, num_q_heads, num_splits]                fp32, log2 domain
  *   block_table[batch, max_blocks]                             int32
  *   seq_lens   [batch]                                         int32
+ *
+ * Size limits (PA_ERR_UNSUPPORTED beyond them): block_size a power of two in
+ * [16, 256]; max_blocks * block_size < 2^31 tokens; one page
+ * (block_size * stride_kt) under 2 GiB and the page stride (stride_kn) under
+ * 4 GiB in bytes, likewise 2 GiB / 4 GiB for the int8 scale pages; the pool
+ * itself (num_blocks pages) may be any size. q, out, k_cache, v_cache and
+ * their strides are 16-byte aligned (PA_ERR_INVALID otherwise).
  */
 #ifndef PAGEDATTN_H_
 #define PAGEDATTN_H_
