@@ -12,6 +12,8 @@ seq_lens), then per layer:
     step before the decode, integration/vllm_backend.py:117-122);
   * runs the decode with a fixed flat split (`flat_splits_for`, no host-side
     lengths, so no device sync).
+With --graph the whole step is captured once as a HIP graph and replayed per
+step, which is how a serving loop removes the per-launch host cost.
 
 TPOT here is the attention share of time per output token: all layers' writes
 and decodes of one step, timed with HIP events. There are no weights, MLPs,
@@ -22,7 +24,7 @@ the flat decode of the last step must agree with the unsplit kernel within
 usage (from the repository root):
   python paged-decode-attention_amd/integration/bench_decode_loop.py \\
       [--shape llama3-8b] [--layers 8] [--requests 64] [--prompt 4096] \\
-      [--output-tokens 64] [--kv fp16] [--out results/decode_loop.json]
+      [--output-tokens 64] [--kv fp16] [--graph] [--out results/decode_loop.json]
 """
 
 from __future__ import annotations
@@ -118,11 +120,45 @@ def run(args, keep_state: bool = False):
     torch.cuda.synchronize()
     counters.update(decode_calls=0, decode_tokens=0)
     events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    if args.graph:
+        # One step as a HIP graph: the step index lives on the device, and
+        # each layer's slot row is selected from it inside the graph, so a
+        # replay needs no host work. Capture records without running.
+        idx = torch.full((1,), w, dtype=torch.long, device=dev)
+        cur = [torch.empty((1, b), dtype=torch.long, device=dev) for _ in layers]
+
+        def graph_step() -> None:
+            lens.add_(1)
+            for (c, slots, q, kv, out), slot in zip(layers, cur):
+                torch.index_select(slots, 0, idx, out=slot)
+                reshape_and_cache(kv[0], kv[1], c, slot[0])
+                paged_decode_hip(q, c, out=out, flat_splits=flat)
+            idx.add_(1)
+
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            graph_step()
+        torch.cuda.synchronize()
+
+        def timed(i: int) -> None:
+            graph.replay()
+            counters["decode_calls"] += len(layers)
+            counters["decode_tokens"] += b * len(layers)
+    else:
+        def timed(i: int) -> None:
+            step(w + i)
+    check_each = getattr(args, "check_each", False)
     t0 = time.perf_counter()
     for i, (e0, e1) in enumerate(events):
         e0.record()
-        step(w + i)
+        timed(i)
         e1.record()
+        if check_each:
+            # every step (every replay) against an eager decode of the same state
+            torch.cuda.synchronize()
+            for c, _, q, _, out in layers:
+                if not torch.equal(out, paged_decode_hip(q, c, flat_splits=flat)):
+                    raise RuntimeError(f"step {i}: output differs from an eager decode of the same state")
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     tpot = sorted(e0.elapsed_time(e1) for e0, e1 in events)
@@ -163,7 +199,8 @@ def run(args, keep_state: bool = False):
         total_tok_per_s=b * n / wall,
         slo_attainment={f"{x:g}ms": sum(1 for t in tpot if t <= x) / len(tpot)
                         for x in [float(v) for v in args.slo.split(",") if v]},
-        tpot_source="HIP events around each step's KV writes and decodes (all layers)",
+        tpot_source=("HIP events around each step's KV writes and decodes (all layers)"
+                     + (", one HIP graph replay per step" if args.graph else ", eager launches")),
         max_model_len=total,
         gpu_memory_utilization=float("nan"),
         note=f"no weights, MLP, sampling or prefill; self-check max |flat - unsplit| = {err:.2e}",
@@ -182,10 +219,13 @@ def main() -> None:
     ap.add_argument("--kv", default="fp16", choices=["fp16", "bf16", "fp8_e5m2", "int8"])
     ap.add_argument("--slo", default="10,20,50,100")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--graph", action="store_true", help="replay each step as one HIP graph")
     ap.add_argument("--out", default=None, help="append the run to this JSON file ({'runs': [...]})")
     args = ap.parse_args()
     if args.output_tokens < 1 or args.prompt < 1 or args.requests < 1 or args.layers < 1:
         raise SystemExit("--output-tokens, --prompt, --requests and --layers must be positive")
+    if args.graph and args.warmup < 1:
+        raise SystemExit("--graph needs --warmup >= 1 (the split workspace is allocated before capture)")
 
     r = run(args)
     print(f"backend            {r.backend}")

@@ -26,11 +26,15 @@ import bench_decode_loop  # noqa: E402
 pytestmark = pytest.mark.gpu
 
 
+@pytest.mark.parametrize("graph", [False, True], ids=["eager", "graph"])
 @pytest.mark.parametrize("kv", ["fp16", "bf16", "fp8_e5m2", "int8"])
-def test_decode_loop_last_step_matches_the_oracle(kv):
+def test_decode_loop_last_step_matches_the_oracle(kv, graph):
+    """With `graph`, every step is one replay of a captured HIP graph. After
+    each step (each replay) the loop synchronises and compares every layer's
+    output with an eager decode of the same state, bit for bit."""
     args = argparse.Namespace(shape="qwen2.5-0.5b", layers=2, requests=5, prompt=77, output_tokens=6,
-                              warmup=2, kv=kv, slo="1,10", seed=3, out=None)
-    print(f"kv={kv}", flush=True)
+                              warmup=2, kv=kv, slo="1,10", seed=3, out=None, graph=graph, check_each=True)
+    print(f"kv={kv} graph={graph}", flush=True)
     r, layers, flat = bench_decode_loop.run(args, keep_state=True)
     assert r.output_tokens == 5 * 6 and r.tpot_ms_p50 > 0
     for c, _, q, _, out in layers:
