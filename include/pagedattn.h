@@ -39,7 +39,8 @@
  *   seq_lens   [batch]                                         int32
  *
  * Size limits (PA_ERR_UNSUPPORTED beyond them): block_size a power of two in
- * [16, 256]; max_blocks * block_size < 2^31 tokens; one page
+ * [16, 256]; max_blocks * block_size < 2^31 tokens; batch * stride_btb < 2^31
+ * block-table entries; one page
  * (block_size * stride_kt) under 2 GiB and the page stride (stride_kn) under
  * 4 GiB in bytes, likewise 2 GiB / 4 GiB for the int8 scale pages; the pool
  * itself (num_blocks pages) may be any size. q, out, k_cache, v_cache and

@@ -147,6 +147,7 @@ INVALID = [
     # page offsets inside a page and page strides are 32-bit in the kernels
     ("page_2gib", dict(stride_kt=2**27, stride_kn=16 * 2**27), _abi.PA_ERR_UNSUPPORTED),
     ("page_stride_4gib", dict(stride_kn=2**31), _abi.PA_ERR_UNSUPPORTED),
+    ("block_table_2pow31", dict(stride_btb=2**30), _abi.PA_ERR_UNSUPPORTED),
     ("scale_page_stride_4gib", dict(kv_dtype=_abi.PA_KV_INT8, scale_dtype=_abi.PA_SCALE_FP32, k_scale=FAKE,
                                     v_scale=FAKE, stride_sn=2**30, stride_st=8), _abi.PA_ERR_UNSUPPORTED),
 ]
