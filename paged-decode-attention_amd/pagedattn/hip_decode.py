@@ -76,12 +76,12 @@ UNSPLIT_MAX_KV_BYTES = {"fp16": 512 << 20, "bf16": 512 << 20, "fp8_e5m2": 192 <<
 # 2048]), flat against unsplit: B = 512 fp16 406 / 415 us, int8 224 / 264;
 # B = 1024 fp16 790 / 794, int8 434 / 490, fp8 425 / 451; B = 2048 fp16
 # 1596 / 1566 ...
+# Even a flat split that needs no merge (every range holds whole sequences)
+# loses to the unsplit kernel above it: graph-timed uniform batches, flat
+# against unsplit, fp16 B = 2048, T = 256 443 / 378 us, B = 4096, T = 128
+# 668 / 489, B = 3072, T = 1024 2200 / 2072; int8 B = 2048, T = 512
+# 469 / 439 (int8 at T = 1024 is the one case within 4% the other way).
 FLAT_MAX_BATCH = 1024
-# ... unless the flat split needs no merge (every range holds whole
-# sequences): then only the decode waves scan, and the flat pass alone beats
-# the unsplit kernel up to this batch (B = 2048, T = 256: fp16 367 / 375 us,
-# int8 223 / 255; B = 4096, T = 128: fp16 399 / 469, int8 257 / 317).
-FLAT_MERGE_FREE_MAX_BATCH = 4096
 
 _KV_CODE = {"fp16": _abi.PA_KV_FP16, "fp8_e5m2": _abi.PA_KV_FP8_E5M2, "int8": _abi.PA_KV_INT8,
             "bf16": _abi.PA_KV_BF16}
@@ -181,8 +181,7 @@ def plan_decode(seq_lens, num_kv_heads: int, group: int, sm_count: int,
     The flat split (one round of waves, `flat_splits_for`) whenever each of
     its waves gets at least MIN_FLAT_TILES_PER_WAVE tiles and the batch is at
     most FLAT_MAX_BATCH: it is balanced for any mix of lengths and measured
-    fastest on every BASELINE split shape (and, when it needs no merge, up to
-    FLAT_MERGE_FREE_MAX_BATCH sequences). Exception, when `kv_dtype` and
+    fastest on every BASELINE split shape. Exception, when `kv_dtype` and
     `head_dim` are given: a nearly uniform batch that fills the CUs unsplit
     stays unsplit (no merge launch) up to UNSPLIT_MAX_KV_BYTES of K/V, unless
     the flat split needs no merge either (`flat_needs_merge`), as for a
@@ -192,8 +191,7 @@ def plan_decode(seq_lens, num_kv_heads: int, group: int, sm_count: int,
     tmax = max(lens) if lens else 0
     flat = flat_splits_for(num_kv_heads, group, sm_count, waves_per_simd)
     tiles = sum(-(-t // TILE_TOKENS) for t in lens)
-    fits = len(lens) <= FLAT_MAX_BATCH or (len(lens) <= FLAT_MERGE_FREE_MAX_BATCH
-                                           and not flat_needs_merge(lens, flat))
+    fits = len(lens) <= FLAT_MAX_BATCH
     if len(lens) == 1 and tmax <= SINGLE_SEQ_SPLIT_MAX_TOKENS:
         fits = False  # the classic split's shorter merge wins
     if fits and tiles >= MIN_FLAT_TILES_PER_WAVE * flat:

@@ -303,7 +303,7 @@ def test_aligned_flat_batch_skips_the_merge():
 
 
 def test_large_uniform_batch_takes_the_merge_free_flat_split():
-    """B = 1024 (above FLAT_MAX_BATCH): each flat range holds 8 whole
+    """B = 1024 (FLAT_MAX_BATCH, the largest flat batch): each flat range holds 8 whole
     sequences, so the planner takes the flat split and the decode pass alone
     writes every output; it agrees with the unsplit kernel on every row and
     with the oracle on sampled rows."""

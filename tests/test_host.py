@@ -372,11 +372,11 @@ def test_flat_splits_for_and_plan_decode():
     from pagedattn.hip_decode import FLAT_MAX_BATCH
     assert plan_decode([4096] * (FLAT_MAX_BATCH + 1), 8, 4, 256, 2)[2] == 0
     assert plan_decode([4096] * FLAT_MAX_BATCH, 8, 4, 256, 2)[2] == 128
-    # ... except a merge-free flat split (whole sequences per range) up to
-    # FLAT_MERGE_FREE_MAX_BATCH
-    from pagedattn.hip_decode import FLAT_MERGE_FREE_MAX_BATCH
-    assert plan_decode([1024] * FLAT_MERGE_FREE_MAX_BATCH, 8, 4, 256, 1)[2] == 128
-    assert plan_decode([1024] * (FLAT_MERGE_FREE_MAX_BATCH + 1), 8, 4, 256, 1)[2] == 0
+    # ... even when the flat split would need no merge (whole sequences per
+    # range): the unsplit kernel is faster there
+    assert plan_decode([1024] * FLAT_MAX_BATCH, 8, 4, 256, 1)[2] == 128
+    assert plan_decode([1024] * (FLAT_MAX_BATCH + 1), 8, 4, 256, 1) == (1, 1024, 0)
+    assert plan_decode([128] * 4096, 8, 4, 256, 1) == (1, 128, 0)
     assert plan_decode([1024, 1056] * (FLAT_MAX_BATCH // 2 + 1), 8, 4, 256, 1)[2] == 0
     assert plan_decode([1024, 1056] * (FLAT_MAX_BATCH // 2), 8, 4, 256, 1)[2] == 128
     # with the KV type known, a nearly uniform batch that fills the CUs
