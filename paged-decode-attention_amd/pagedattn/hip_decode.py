@@ -68,6 +68,15 @@ SINGLE_SEQ_SPLIT_MAX_TOKENS = 65536
 # at 537 MB, 166 / 162 at 1074 MB; fp8 26.6 / 29.0 at 134 MB, 49.5 / 47.2 at
 # 268 MB; int8 18.2 / 19.5 at 67 MB, 24.5 / 24.6 at 101 MB, 31.4 / 29.6 at
 # 134 MB.
+# With 2-byte KV, a nearly uniform batch that fills the CUs unsplit also
+# runs unsplit, whatever its size, while its longest sequence has at most
+# this many tokens. The flat split loses there even without a merge, because
+# its waves switch sequences every few tiles. Graph-timed whole calls,
+# flat against unsplit, fp16: B = 128, T = 256 29.0 / 26.1 us, T = 1024 90.1
+# / 87.6, T = 2048 170.8 / 170.8; B = 512, T = 512 182.9 / 177.4; B = 1024,
+# T = 256 208.9 / 189.2, T = 1024 700.4 / 689.9, T = 2048 1355 / 1363; bf16
+# the same. 1-byte KV keeps the flat split (int8 B = 512, T = 256 64.3 / 73.4).
+UNSPLIT_2B_MAX_TOKENS = 1024
 UNSPLIT_MAX_KV_BYTES = {"fp16": 512 << 20, "bf16": 512 << 20, "fp8_e5m2": 192 << 20,
                         "int8": 96 << 20}
 # Every flat wave and every merge wave scans seq_lens (512 lengths per round
@@ -181,11 +190,12 @@ def plan_decode(seq_lens, num_kv_heads: int, group: int, sm_count: int,
     The flat split (one round of waves, `flat_splits_for`) whenever each of
     its waves gets at least MIN_FLAT_TILES_PER_WAVE tiles and the batch is at
     most FLAT_MAX_BATCH: it is balanced for any mix of lengths and measured
-    fastest on every BASELINE split shape. Exception, when `kv_dtype` and
-    `head_dim` are given: a nearly uniform batch that fills the CUs unsplit
-    stays unsplit (no merge launch) up to UNSPLIT_MAX_KV_BYTES of K/V, unless
-    the flat split needs no merge either (`flat_needs_merge`), as for a
-    uniform batch of 128 at F = 128. Smaller batches take `plan_num_splits`.
+    fastest on every BASELINE split shape. Exceptions, when `kv_dtype` and
+    `head_dim` are given, for a nearly uniform batch that fills the CUs
+    unsplit: with 2-byte KV and sequences of at most UNSPLIT_2B_MAX_TOKENS it
+    runs unsplit; otherwise it stays unsplit (no merge launch) up to
+    UNSPLIT_MAX_KV_BYTES of K/V, unless the flat split needs no merge either
+    (`flat_needs_merge`). Smaller batches take `plan_num_splits`.
     """
     lens = [max(0, int(t)) for t in seq_lens]
     tmax = max(lens) if lens else 0
@@ -195,11 +205,13 @@ def plan_decode(seq_lens, num_kv_heads: int, group: int, sm_count: int,
     if len(lens) == 1 and tmax <= SINGLE_SEQ_SPLIT_MAX_TOKENS:
         fits = False  # the classic split's shorter merge wins
     if fits and tiles >= MIN_FLAT_TILES_PER_WAVE * flat:
-        if kv_dtype is not None and head_dim is not None and flat_needs_merge(lens, flat):
+        if kv_dtype is not None and head_dim is not None and _fills_unsplit(lens, num_kv_heads, group,
+                                                                             sm_count):
             elem = 1 if kv_dtype in ("fp8_e5m2", "int8") else 2
+            if elem == 2 and tmax <= UNSPLIT_2B_MAX_TOKENS:
+                return 1, tmax, 0
             kv_bytes = sum(lens) * num_kv_heads * head_dim * elem * 2
-            if (kv_bytes <= UNSPLIT_MAX_KV_BYTES.get(kv_dtype, 0)
-                    and _fills_unsplit(lens, num_kv_heads, group, sm_count)):
+            if kv_bytes <= UNSPLIT_MAX_KV_BYTES.get(kv_dtype, 0) and flat_needs_merge(lens, flat):
                 return 1, tmax, 0
         return 1, tmax, flat
     splits, tmax = plan_num_splits(lens, num_kv_heads, group, sm_count)

@@ -312,9 +312,10 @@ def test_large_uniform_batch_takes_the_merge_free_flat_split():
     from pagedattn.hip_decode import _cu_count
 
     lens = [256] * 1024
-    c = allocate(LLAMA3_8B, len(lens), lens, seed=43, device="cuda", fill_device="cuda")
+    # int8: with 2-byte KV a batch of short sequences like this one runs unsplit
+    c = allocate(LLAMA3_8B, len(lens), lens, seed=43, device="cuda", fill_device="cuda", kv_dtype="int8")
     q = seeded_q(len(lens), 32, 128, 43, device="cuda")
-    planned = plan_decode(lens, 8, 4, _cu_count(q.device), 1, kv_dtype="fp16", head_dim=128)
+    planned = plan_decode(lens, 8, 4, _cu_count(q.device), 1, kv_dtype="int8", head_dim=128)
     print(f"plan {planned}")
     if planned[2] == 0 or flat_needs_merge(lens, planned[2]):
         pytest.skip(f"the plan {planned} is not a merge-free flat split on this GPU")

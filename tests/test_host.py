@@ -390,8 +390,18 @@ def test_flat_splits_for_and_plan_decode():
     assert plan_decode([2048] * 64, 8, 4, 256, 1, kv_dtype="fp8_e5m2", head_dim=128)[2] == 128
     assert plan_decode([1024] * 64, 8, 4, 256, 1, kv_dtype="int8", head_dim=128)[2] == 128
     # ... and so does a batch the flat split covers with no merge (B = 128, F = 128:
-    # one sequence per range), which streams faster than the unsplit kernel
-    assert plan_decode([512] * 128, 8, 4, 256, 1, kv_dtype="fp16", head_dim=128) == (1, 512, 128)
+    # one sequence per range) when its sequences are long or its KV 1-byte
+    assert plan_decode([2048] * 128, 8, 4, 256, 1, kv_dtype="fp16", head_dim=128) == (1, 2048, 128)
+    assert plan_decode([512] * 128, 8, 4, 256, 1, kv_dtype="int8", head_dim=128) == (1, 512, 128)
+    # with 2-byte KV and sequences of at most UNSPLIT_2B_MAX_TOKENS the unsplit
+    # kernel wins at any size, merge or not
+    from pagedattn.hip_decode import UNSPLIT_2B_MAX_TOKENS
+    assert plan_decode([512] * 128, 8, 4, 256, 1, kv_dtype="fp16", head_dim=128) == (1, 512, 0)
+    assert plan_decode([UNSPLIT_2B_MAX_TOKENS] * 1024, 8, 4, 256, 1, kv_dtype="bf16",
+                       head_dim=128) == (1, UNSPLIT_2B_MAX_TOKENS, 0)
+    assert plan_decode([UNSPLIT_2B_MAX_TOKENS + 32] * 1024, 8, 4, 256, 1, kv_dtype="fp16",
+                       head_dim=128)[2] == 128
+    assert plan_decode([256] * 512, 8, 4, 256, 1, kv_dtype="fp8_e5m2", head_dim=128)[2] == 128
     # a ragged batch of the same size, or one that does not fill the CUs, too
     ragged = [256, 1792] * 32
     assert plan_decode(ragged, 8, 4, 256, 1, kv_dtype="fp16", head_dim=128)[2] == 128
