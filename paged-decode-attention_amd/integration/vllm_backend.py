@@ -47,6 +47,7 @@ from pagedattn.hip_decode import (  # noqa: E402
     TILE_TOKENS,
     flat_splits_for,
     flat_waves_per_simd,
+    short_batch_runs_unsplit,
 )
 from pagedattn.triton_decode import paged_decode_triton, pick_num_splits  # noqa: E402
 
@@ -163,17 +164,21 @@ def decode_forward(impl, layer, query, key, value, kv_cache, attn_metadata, outp
     # Host-side only (no device sync): max_seq_len is a host int in the
     # metadata. The flat split needs no lengths; it is taken when the batch
     # can hold enough tiles for its waves (the upper bound
-    # n * ceil(max_seq_len / 32) against plan_decode's threshold), otherwise
-    # the classic split, chunked from the longest sequence.
+    # n * ceil(max_seq_len / 32) against plan_decode's threshold) and is not
+    # a large batch of short sequences (plan_decode's ragged rule, which
+    # needs only n and max_seq_len), otherwise the classic split, chunked
+    # from the longest sequence.
     msl = int(attn_metadata.max_seq_len)
     group = impl.num_heads // impl.num_kv_heads
-    flat = flat_splits_for(impl.num_kv_heads, group, _cu_count(query.device),
-                           flat_waves_per_simd(cache.kv_dtype, impl.head_size))
+    cus = _cu_count(query.device)
+    flat = flat_splits_for(impl.num_kv_heads, group, cus, flat_waves_per_simd(cache.kv_dtype, impl.head_size))
     single = n == 1 and msl <= SINGLE_SEQ_SPLIT_MAX_TOKENS  # plan_decode's single-sequence rule
-    if not single and n <= FLAT_MAX_BATCH and n * -(-msl // TILE_TOKENS) >= MIN_FLAT_TILES_PER_WAVE * flat:
+    short = short_batch_runs_unsplit(n, msl, impl.num_kv_heads, group, cus, cache.kv_dtype)
+    if (not single and not short and n <= FLAT_MAX_BATCH
+            and n * -(-msl // TILE_TOKENS) >= MIN_FLAT_TILES_PER_WAVE * flat):
         decode(query[:n], cache, out=output[:n], sm_scale=impl.scale, flat_splits=flat)
     else:
-        splits = pick_num_splits(n, impl.num_kv_heads, msl, _cu_count(query.device))
+        splits = pick_num_splits(n, impl.num_kv_heads, msl, cus)
         decode(query[:n], cache, out=output[:n], num_splits=splits, sm_scale=impl.scale,
                max_seq_len=msl)
     STATS["decode_calls"] += 1

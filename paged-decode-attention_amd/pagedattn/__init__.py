@@ -20,6 +20,7 @@ from .hip_decode import (
     pick_num_splits,
     plan_decode,
     plan_num_splits,
+    short_batch_runs_unsplit,
     split_reduce,
 )
 
@@ -28,6 +29,6 @@ __all__ = [
     "kv_bytes_per_token",
     "PagedKVCache", "allocate", "quantize_kv", "reshape_and_cache",
     "paged_decode_hip", "paged_decode_triton", "pick_num_splits", "plan_num_splits",
-    "plan_decode", "flat_needs_merge", "flat_splits_for", "flat_waves_per_simd",
+    "plan_decode", "short_batch_runs_unsplit", "flat_needs_merge", "flat_splits_for", "flat_waves_per_simd",
     "decode_partials", "split_reduce",
 ]

@@ -68,15 +68,28 @@ SINGLE_SEQ_SPLIT_MAX_TOKENS = 65536
 # at 537 MB, 166 / 162 at 1074 MB; fp8 26.6 / 29.0 at 134 MB, 49.5 / 47.2 at
 # 268 MB; int8 18.2 / 19.5 at 67 MB, 24.5 / 24.6 at 101 MB, 31.4 / 29.6 at
 # 134 MB.
-# With 2-byte KV, a nearly uniform batch that fills the CUs unsplit also
-# runs unsplit, whatever its size, while its longest sequence has at most
-# this many tokens. The flat split loses there even without a merge, because
-# its waves switch sequences every few tiles. Graph-timed whole calls,
-# flat against unsplit, fp16: B = 128, T = 256 29.0 / 26.1 us, T = 1024 90.1
-# / 87.6, T = 2048 170.8 / 170.8; B = 512, T = 512 182.9 / 177.4; B = 1024,
-# T = 256 208.9 / 189.2, T = 1024 700.4 / 689.9, T = 2048 1355 / 1363; bf16
-# the same. 1-byte KV keeps the flat split (int8 B = 512, T = 256 64.3 / 73.4).
-UNSPLIT_2B_MAX_TOKENS = 1024
+# Batches of short sequences that fill the CUs run unsplit, whatever their
+# size and merge or not: the flat split loses there, because its waves
+# switch sequences every few tiles. Per KV type, the longest sequence of a
+# nearly uniform batch (UNSPLIT_SHORT_MAX_TOKENS), or of a ragged batch with
+# at least RAGGED_UNSPLIT_MIN_WGS_PER_CU unsplit workgroups per CU
+# (UNSPLIT_RAGGED_MAX_TOKENS). Graph-timed whole calls at the Llama-3-8B
+# shape (g = 4, D = 128, 256 CUs), flat against unsplit, in us:
+#   fp16 uniform: B = 128, T = 256 29.0 / 26.1, T = 1024 90.1 / 87.6, T = 2048
+#     170.8 / 170.8; B = 1024, T = 256 208.9 / 189.2, T = 1024 700.4 / 689.9,
+#     T = 2048 1355 / 1363 (bf16 the same);
+#   fp16 ragged, T ~ U[32, hi]: B = 256, hi = 512 61.0 / 56.2, hi = 1024 102.3
+#     / 101.1, hi = 2048 190.5 / 198.5; B = 1024, hi = 512 233.8 / 211.8,
+#     hi = 1024 389.7 / 371.8, hi = 2048 711.0 / 707.2; B = 128 (4 workgroups
+#     per CU), hi = 1024: 0.93 x the unsplit time;
+#   fp8 uniform: B = 128, T = 256 19.2 / 16.4, T = 512 30.1 / 29.3, T = 1024
+#     50.5 / 52.0; B = 512, T = 256 59.5 / 58.2, T = 512 0.96 x;
+#   fp8 ragged: B = 256, hi = 512 39.4 / 35.2; B = 1024, hi = 256 97.4 / 80.3,
+#     hi = 512 141.5 / 128.9;
+#   int8 keeps the flat split (uniform B = 512, T = 256 64.3 / 73.4).
+UNSPLIT_SHORT_MAX_TOKENS = {"fp16": 1024, "bf16": 1024, "fp8_e5m2": 256}
+UNSPLIT_RAGGED_MAX_TOKENS = {"fp16": 1024, "bf16": 1024, "fp8_e5m2": 512}
+RAGGED_UNSPLIT_MIN_WGS_PER_CU = 8
 UNSPLIT_MAX_KV_BYTES = {"fp16": 512 << 20, "bf16": 512 << 20, "fp8_e5m2": 192 << 20,
                         "int8": 96 << 20}
 # Every flat wave and every merge wave scans seq_lens (512 lengths per round
@@ -130,6 +143,26 @@ def _fills_unsplit(lens: list[int], num_kv_heads: int, group: int, sm_count: int
         return False
     units = num_kv_heads * -(-group // _abi.PA_MAX_GROUP)
     return len(lens) * units >= max(1, sm_count) and max(lens) <= 1.25 * sum(lens) / len(lens)
+
+
+def short_batch_runs_unsplit(batch: int, max_seq_len: int, num_kv_heads: int, group: int,
+                             sm_count: int, kv_dtype: str, uniform: bool = False) -> bool:
+    """Whether a batch of short sequences runs faster unsplit than flat.
+
+    With `uniform` (a nearly uniform batch whose unsplit workgroups give every
+    CU one, `_fills_unsplit`) the longest sequence may have up to
+    UNSPLIT_SHORT_MAX_TOKENS; any batch with RAGGED_UNSPLIT_MIN_WGS_PER_CU
+    unsplit workgroups per CU up to UNSPLIT_RAGGED_MAX_TOKENS. Needs only the
+    batch size and the longest length, so a caller without the lengths (the
+    vLLM boundary) applies the ragged rule.
+    """
+    if max_seq_len <= 0:
+        return False
+    if uniform and max_seq_len <= UNSPLIT_SHORT_MAX_TOKENS.get(kv_dtype, 0):
+        return True
+    units = num_kv_heads * -(-group // _abi.PA_MAX_GROUP)
+    return (batch * units >= RAGGED_UNSPLIT_MIN_WGS_PER_CU * max(1, sm_count)
+            and max_seq_len <= UNSPLIT_RAGGED_MAX_TOKENS.get(kv_dtype, 0))
 
 
 def plan_num_splits(seq_lens, num_kv_heads: int, group: int, sm_count: int) -> tuple[int, int]:
@@ -191,11 +224,11 @@ def plan_decode(seq_lens, num_kv_heads: int, group: int, sm_count: int,
     its waves gets at least MIN_FLAT_TILES_PER_WAVE tiles and the batch is at
     most FLAT_MAX_BATCH: it is balanced for any mix of lengths and measured
     fastest on every BASELINE split shape. Exceptions, when `kv_dtype` and
-    `head_dim` are given, for a nearly uniform batch that fills the CUs
-    unsplit: with 2-byte KV and sequences of at most UNSPLIT_2B_MAX_TOKENS it
-    runs unsplit; otherwise it stays unsplit (no merge launch) up to
-    UNSPLIT_MAX_KV_BYTES of K/V, unless the flat split needs no merge either
-    (`flat_needs_merge`). Smaller batches take `plan_num_splits`.
+    `head_dim` are given: a batch of short sequences that fills the CUs runs
+    unsplit (`short_batch_runs_unsplit`); a nearly uniform batch that fills
+    the CUs unsplit stays unsplit (no merge launch) up to UNSPLIT_MAX_KV_BYTES
+    of K/V, unless the flat split needs no merge either (`flat_needs_merge`).
+    Smaller batches take `plan_num_splits`.
     """
     lens = [max(0, int(t)) for t in seq_lens]
     tmax = max(lens) if lens else 0
@@ -205,13 +238,14 @@ def plan_decode(seq_lens, num_kv_heads: int, group: int, sm_count: int,
     if len(lens) == 1 and tmax <= SINGLE_SEQ_SPLIT_MAX_TOKENS:
         fits = False  # the classic split's shorter merge wins
     if fits and tiles >= MIN_FLAT_TILES_PER_WAVE * flat:
-        if kv_dtype is not None and head_dim is not None and _fills_unsplit(lens, num_kv_heads, group,
-                                                                             sm_count):
-            elem = 1 if kv_dtype in ("fp8_e5m2", "int8") else 2
-            if elem == 2 and tmax <= UNSPLIT_2B_MAX_TOKENS:
+        if kv_dtype is not None and head_dim is not None:
+            fills = _fills_unsplit(lens, num_kv_heads, group, sm_count)
+            if short_batch_runs_unsplit(len(lens), tmax, num_kv_heads, group, sm_count, kv_dtype,
+                                        uniform=fills):
                 return 1, tmax, 0
+            elem = 1 if kv_dtype in ("fp8_e5m2", "int8") else 2
             kv_bytes = sum(lens) * num_kv_heads * head_dim * elem * 2
-            if kv_bytes <= UNSPLIT_MAX_KV_BYTES.get(kv_dtype, 0) and flat_needs_merge(lens, flat):
+            if fills and kv_bytes <= UNSPLIT_MAX_KV_BYTES.get(kv_dtype, 0) and flat_needs_merge(lens, flat):
                 return 1, tmax, 0
         return 1, tmax, flat
     splits, tmax = plan_num_splits(lens, num_kv_heads, group, sm_count)

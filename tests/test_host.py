@@ -393,16 +393,32 @@ def test_flat_splits_for_and_plan_decode():
     # one sequence per range) when its sequences are long or its KV 1-byte
     assert plan_decode([2048] * 128, 8, 4, 256, 1, kv_dtype="fp16", head_dim=128) == (1, 2048, 128)
     assert plan_decode([512] * 128, 8, 4, 256, 1, kv_dtype="int8", head_dim=128) == (1, 512, 128)
-    # with 2-byte KV and sequences of at most UNSPLIT_2B_MAX_TOKENS the unsplit
-    # kernel wins at any size, merge or not
-    from pagedattn.hip_decode import UNSPLIT_2B_MAX_TOKENS
+    # a batch of short sequences that fills the CUs runs unsplit at any size,
+    # merge or not: nearly uniform up to UNSPLIT_SHORT_MAX_TOKENS ...
+    from pagedattn.hip_decode import (RAGGED_UNSPLIT_MIN_WGS_PER_CU, UNSPLIT_RAGGED_MAX_TOKENS,
+                                      UNSPLIT_SHORT_MAX_TOKENS)
     assert plan_decode([512] * 128, 8, 4, 256, 1, kv_dtype="fp16", head_dim=128) == (1, 512, 0)
-    assert plan_decode([UNSPLIT_2B_MAX_TOKENS] * 1024, 8, 4, 256, 1, kv_dtype="bf16",
-                       head_dim=128) == (1, UNSPLIT_2B_MAX_TOKENS, 0)
-    assert plan_decode([UNSPLIT_2B_MAX_TOKENS + 32] * 1024, 8, 4, 256, 1, kv_dtype="fp16",
-                       head_dim=128)[2] == 128
-    assert plan_decode([256] * 512, 8, 4, 256, 1, kv_dtype="fp8_e5m2", head_dim=128)[2] == 128
-    # a ragged batch of the same size, or one that does not fill the CUs, too
+    t16, t8 = UNSPLIT_SHORT_MAX_TOKENS["fp16"], UNSPLIT_SHORT_MAX_TOKENS["fp8_e5m2"]
+    assert plan_decode([t16] * 1024, 8, 4, 256, 1, kv_dtype="bf16", head_dim=128) == (1, t16, 0)
+    assert plan_decode([t16 + 32] * 1024, 8, 4, 256, 1, kv_dtype="fp16", head_dim=128)[2] == 128
+    assert plan_decode([t8] * 512, 8, 4, 256, 1, kv_dtype="fp8_e5m2", head_dim=128) == (1, t8, 0)
+    assert plan_decode([t8] * 128, 8, 4, 256, 1, kv_dtype="fp8_e5m2", head_dim=128) == (1, t8, 0)
+    assert plan_decode([t8 + 256] * 128, 8, 4, 256, 1, kv_dtype="fp8_e5m2", head_dim=128)[2] == 128
+    # ... int8 never ...
+    assert plan_decode([256] * 512, 8, 4, 256, 1, kv_dtype="int8", head_dim=128)[2] == 128
+    # ... and ragged, with RAGGED_UNSPLIT_MIN_WGS_PER_CU workgroups per CU, up to
+    # UNSPLIT_RAGGED_MAX_TOKENS
+    nb = RAGGED_UNSPLIT_MIN_WGS_PER_CU * 256 // 8
+    r16, r8 = UNSPLIT_RAGGED_MAX_TOKENS["fp16"], UNSPLIT_RAGGED_MAX_TOKENS["fp8_e5m2"]
+    ramp16 = [32 + (r16 - 32) * i // (nb - 1) for i in range(nb)]
+    ramp8 = [32 + (r8 - 32) * i // (nb - 1) for i in range(nb)]
+    assert max(ramp16) == r16 and max(ramp8) == r8
+    assert plan_decode(ramp16, 8, 4, 256, 1, kv_dtype="fp16", head_dim=128) == (1, r16, 0)
+    assert plan_decode(ramp8, 8, 4, 256, 1, kv_dtype="fp8_e5m2", head_dim=128) == (1, r8, 0)
+    assert plan_decode(ramp16[:-1] + [r16 + 1], 8, 4, 256, 1, kv_dtype="fp16", head_dim=128)[2] == 128
+    assert plan_decode(ramp16[: nb - 8], 8, 4, 256, 1, kv_dtype="fp16", head_dim=128)[2] == 128
+    assert plan_decode(ramp8, 8, 4, 256, 1, kv_dtype="int8", head_dim=128)[2] == 128
+    # a smaller ragged batch, or one that does not fill the CUs, keeps the flat split
     ragged = [256, 1792] * 32
     assert plan_decode(ragged, 8, 4, 256, 1, kv_dtype="fp16", head_dim=128)[2] == 128
     assert plan_decode([8192] * 8, 8, 4, 256, 1, kv_dtype="fp16", head_dim=128)[2] == 128

@@ -213,3 +213,39 @@ def test_decode_forward_takes_the_flat_split_for_large_batches(monkeypatch):
     vb.decode_forward(impl, None, q[:1], q[:1], q[:1], _kv(), meta, torch.zeros_like(q[:1]),
                       decode=fake_decode)
     assert calls[-1] == {"num_splits": vb.pick_num_splits(1, 8, 16384, 256), "max_seq_len": 16384}
+
+
+@pytest.mark.parametrize("dtype,limit", [(torch.float16, 1024), (torch.bfloat16, 1024)],
+                         ids=["fp16", "bf16"])
+def test_decode_forward_runs_large_short_batches_unsplit(monkeypatch, dtype, limit):
+    """Host-side routing only: a batch with 8 unsplit workgroups per CU whose
+    longest sequence has at most the KV type's ragged limit runs unsplit;
+    one token more takes the flat split. (The boundary serves 2-byte caches
+    only, as the reference's backend does.)"""
+    monkeypatch.setattr(vb, "_cu_count", lambda dev: 256)
+    monkeypatch.setattr(vb, "flat_waves_per_simd", lambda kv, d: 1)
+    calls = []
+
+    def fake_decode(q, cache, out, sm_scale, **kw):
+        calls.append(kw)
+
+    impl = FakeBaseImpl()
+    impl.kv_sharing_target_layer_name = "shared"
+    n = 256  # 8 kv heads, group 4: 2048 workgroups = 8 per CU
+    q = torch.randn(n, 32, 128).half()
+    for msl, want_flat in ((limit, False), (limit + 1, True)):
+        meta = _meta(num_actual_tokens=n, max_seq_len=msl,
+                     block_table=torch.zeros((n, 80), dtype=torch.int32),
+                     seq_lens=torch.full((n,), msl, dtype=torch.int32))
+        vb.decode_forward(impl, None, q, q, q, _kv(dtype), meta, torch.zeros_like(q), decode=fake_decode)
+        if want_flat:
+            assert calls[-1] == {"flat_splits": vb.flat_splits_for(8, 4, 256, 1)}
+        else:
+            assert calls[-1] == {"num_splits": 1, "max_seq_len": msl}
+    # half the batch (4 workgroups per CU) keeps the flat split
+    meta = _meta(num_actual_tokens=n // 2, max_seq_len=limit,
+                 block_table=torch.zeros((n // 2, 80), dtype=torch.int32),
+                 seq_lens=torch.full((n // 2,), limit, dtype=torch.int32))
+    vb.decode_forward(impl, None, q[: n // 2], q[: n // 2], q[: n // 2], _kv(dtype), meta,
+                      torch.zeros_like(q[: n // 2]), decode=fake_decode)
+    assert calls[-1] == {"flat_splits": vb.flat_splits_for(8, 4, 256, 1)}
