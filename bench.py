@@ -269,8 +269,8 @@ def main() -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the decode shards over (batch, kv_head) with no exchange; see the "
-              "sharding notes in DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "(the decode would shard over (batch, kv_head) with no exchange between "
+              "GPUs). Run with --gpus 1.", file=sys.stderr)
         return 2
 
     import torch

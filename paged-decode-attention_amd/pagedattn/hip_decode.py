@@ -47,7 +47,7 @@ RAGGED_SPLIT_MIN_TOKENS = 1024
 
 # Flat split: one round of waves, at most FLAT_WAVES_PER_SIMD per SIMD even
 # where the registers allow more. One streaming wave per SIMD measured
-# fastest on every BASELINE split shape: with two, each SIMD's older wave
+# fastest on every benchmark config with a split (C2-C5): with two, each SIMD's older wave
 # runs ahead and the younger ones form a tail (C2 158.5 us at 1, 159.6 at 2;
 # C3 39.3 and 40.6; C5 312.7 and 316.5; three per SIMD or a second round is
 # slower still). Used when each wave gets at least MIN_FLAT_TILES_PER_WAVE
@@ -223,7 +223,7 @@ def plan_decode(seq_lens, num_kv_heads: int, group: int, sm_count: int,
     The flat split (one round of waves, `flat_splits_for`) whenever each of
     its waves gets at least MIN_FLAT_TILES_PER_WAVE tiles and the batch is at
     most FLAT_MAX_BATCH: it is balanced for any mix of lengths and measured
-    fastest on every BASELINE split shape. Exceptions, when `kv_dtype` and
+    fastest on every benchmark config with a split (C2-C5). Exceptions, when `kv_dtype` and
     `head_dim` are given: a batch of short sequences that fills the CUs runs
     unsplit (`short_batch_runs_unsplit`); a nearly uniform batch that fills
     the CUs unsplit stays unsplit (no merge launch) up to UNSPLIT_MAX_KV_BYTES

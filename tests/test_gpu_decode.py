@@ -70,7 +70,7 @@ def test_quantized_kv(kv_dtype, num_splits):
 
 @pytest.mark.parametrize("num_splits", [1, 5])
 def test_int8_fp32_scales(num_splits):
-    """int8 with fp32 per-(token, head) scales (the BASELINE int8 config)."""
+    """int8 with fp32 per-(token, head) scales (the C4 benchmark config)."""
     q, c = _qkv(2, 1500, kv_dtype="int8", scale_dtype=torch.float32, shape=LLAMA3_70B, seed=4)
     ref = oracle.reference_decode(q, c, out_dtype=torch.float32)
     got = paged_decode_hip(q, c, num_splits=num_splits)

@@ -304,7 +304,8 @@ def test_allocate_is_deterministic_and_well_formed():
 
 
 def test_algorithmic_bytes_of_baseline_configs():
-    """BASELINE.md's per-call byte counts, from the same formula bench.py uses."""
+    """The published per-call byte counts of the benchmark configs, from the
+    same formula bench.py uses."""
     import bench
 
     def fake(shape, lens, kv, scale_dt=None):
@@ -360,7 +361,7 @@ def test_flat_splits_for_and_plan_decode():
     assert flat_splits_for(8, 4, 256, 1) == 128
     assert flat_splits_for(2, 20, 256, 2) == 256      # group 20: two head tiles
     assert flat_splits_for(64, 1, 4, 1) == 1
-    # every BASELINE split shape takes the flat split ...
+    # every benchmark config with a split (C2-C5) takes the flat split ...
     assert plan_decode([4096] * 64, 8, 4, 256, 2) == (1, 4096, 128)
     assert plan_decode([16384] * 32, 8, 8, 256, 3) == (1, 16384, 128)
     assert plan_decode([131072] * 4, 8, 4, 256, 2) == (1, 131072, 128)
