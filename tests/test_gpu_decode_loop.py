@@ -2,8 +2,9 @@
 
 integration/bench_decode_loop.py runs the attention part of decode steps: each
 step adds one token to every sequence on the device, and per layer writes the
-new token's K/V (pa_cache_write) and decodes with a fixed flat split
-(pa_decode), with no host-side lengths. A short loop here must leave caches
+new token's K/V (pa_cache_write) and decodes (pa_decode) with no host-side
+lengths: with the flat split, or unsplit for a large batch of short sequences,
+as the vLLM boundary picks. A short loop here must leave caches
 whose last step's output, as the loop computed it, matches the fp32 oracle
 (pagedattn/reference.py:28-49 restated) within 2e-3 for every KV dtype (the
 writer itself is checked bit for bit in test_gpu_cache_write.py).
@@ -35,12 +36,39 @@ def test_decode_loop_last_step_matches_the_oracle(kv, graph):
     args = argparse.Namespace(shape="qwen2.5-0.5b", layers=2, requests=5, prompt=77, output_tokens=6,
                               warmup=2, kv=kv, slo="1,10", seed=3, out=None, graph=graph, check_each=True)
     print(f"kv={kv} graph={graph}", flush=True)
-    r, layers, flat = bench_decode_loop.run(args, keep_state=True)
+    r, layers, launch = bench_decode_loop.run(args, keep_state=True)
+    assert "flat_splits" in launch
     assert r.output_tokens == 5 * 6 and r.tpot_ms_p50 > 0
     for c, _, q, _, out in layers:
         assert c.seq_lens.tolist() == [77 + 2 + 6] * 5
         want = oracle.reference_decode(q.cpu(), c, out_dtype=torch.float32)
         err = (out.float().cpu() - want).abs()
         bound = 2e-3 + (2.0 ** -8 * want.abs() if q.dtype == torch.bfloat16 else 0.0)
-        print(f"  max_abs={err.max().item():.2e} (F={flat})", flush=True)
+        print(f"  max_abs={err.max().item():.2e} ({launch})", flush=True)
         assert bool((err <= bound).all())
+
+
+@pytest.mark.parametrize("graph", [False, True], ids=["eager", "graph"])
+@pytest.mark.parametrize("kv", ["fp16", "fp8_e5m2"])
+def test_decode_loop_of_a_large_short_batch_runs_unsplit(kv, graph):
+    """256 sequences growing from 71 to 75 tokens at the Llama-3-8B shape: 8 unsplit
+    workgroups per CU at 256 CUs, so the loop launches the unsplit kernel, as
+    the vLLM boundary would; every step is checked against an eager decode and
+    sampled rows of the last step against the oracle."""
+    from helpers import subset_cache
+    from pagedattn.hip_decode import _cu_count
+
+    if _cu_count(torch.device("cuda:0")) != 256:
+        pytest.skip("the batch is sized for 256 CUs")
+    args = argparse.Namespace(shape="llama3-8b", layers=1, requests=256, prompt=70, output_tokens=4,
+                              warmup=1, kv=kv, slo="1,10", seed=4, out=None, graph=graph, check_each=True)
+    print(f"kv={kv} graph={graph}", flush=True)
+    r, layers, launch = bench_decode_loop.run(args, keep_state=True)
+    assert launch == {"num_splits": 1, "max_seq_len": 75}
+    c, _, q, _, out = layers[0]
+    assert c.seq_lens.tolist() == [75] * 256
+    rows = [0, 100, 255]
+    want = oracle.reference_decode(q[rows].cpu(), subset_cache(c, rows), out_dtype=torch.float32)
+    err = (out[rows].float().cpu() - want).abs().max().item()
+    print(f"  max_abs={err:.2e} ({launch})", flush=True)
+    assert err < 2e-3
