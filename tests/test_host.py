@@ -456,3 +456,34 @@ def test_flat_merge_needs_flat_splits():
     a = _valid_args(part_out=FAKE, part_lse=FAKE, stride_pb=32 * 128, stride_ph=128)
     assert lib.pa_flat_merge(ctypes.byref(a), None) == _abi.PA_ERR_INVALID
     assert "flat_splits" in lib.pa_last_error().decode()
+
+
+def test_short_batch_runs_unsplit_thresholds():
+    """The short-batch rule on its own: per-KV-type token limits, the
+    workgroups-per-CU threshold scaling with the CU count, and head tiles
+    (groups above PA_MAX_GROUP) counting as extra workgroups."""
+    from pagedattn import short_batch_runs_unsplit as sbu
+    from pagedattn.hip_decode import (RAGGED_UNSPLIT_MIN_WGS_PER_CU, UNSPLIT_RAGGED_MAX_TOKENS,
+                                      UNSPLIT_SHORT_MAX_TOKENS, _abi)
+
+    cus = 256
+    nb = RAGGED_UNSPLIT_MIN_WGS_PER_CU * cus // 8  # 8 kv heads, group 4: one unit per kv head
+    for kv, lim in UNSPLIT_RAGGED_MAX_TOKENS.items():
+        assert sbu(nb, lim, 8, 4, cus, kv)
+        assert not sbu(nb, lim + 1, 8, 4, cus, kv)
+        assert not sbu(nb - 1, lim, 8, 4, cus, kv)
+    for kv, lim in UNSPLIT_SHORT_MAX_TOKENS.items():
+        # nearly uniform batches need only fill the CUs (the caller's check)
+        assert sbu(1, lim, 8, 4, cus, kv, uniform=True)
+        assert not sbu(1, lim + 1, 8, 4, cus, kv, uniform=True)  # a batch of 1 is not ragged-large
+    # int8, unknown types and empty batches never
+    assert not sbu(4 * nb, 64, 8, 4, cus, "int8")
+    assert not sbu(4 * nb, 64, 8, 4, cus, "int8", uniform=True)
+    assert not sbu(nb, 0, 8, 4, cus, "fp16")
+    # twice the CUs need twice the batch
+    assert not sbu(nb, 512, 8, 4, 2 * cus, "fp16")
+    assert sbu(2 * nb, 512, 8, 4, 2 * cus, "fp16")
+    # a group above PA_MAX_GROUP takes two head tiles per kv head
+    g2 = _abi.PA_MAX_GROUP + 1
+    assert sbu(nb // 2, 512, 8, g2, cus, "fp16")
+    assert not sbu(nb // 2, 512, 8, 4, cus, "fp16")
