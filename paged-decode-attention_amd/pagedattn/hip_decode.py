@@ -87,9 +87,17 @@ SINGLE_SEQ_SPLIT_MAX_TOKENS = 65536
 #   fp8 ragged: B = 256, hi = 512 39.4 / 35.2; B = 1024, hi = 256 97.4 / 80.3,
 #     hi = 512 141.5 / 128.9;
 #   int8 keeps the flat split (uniform B = 512, T = 256 64.3 / 73.4).
+# With WIDE_GROUP_MIN or more q heads per kv head both limits double: at the
+# Llama-3-70B shape (g = 8) and the Qwen2.5-0.5B shape (g = 7, D = 64) the
+# unsplit kernel still wins at twice them (ragged, flat against unsplit:
+# 70B B = 256 fp16 hi = 2048 191.2 / 185.2, fp8 hi = 1024 68.5 / 64.8;
+# 70B B = 1024 fp16 hi = 2048 777.9 / 747.2, fp8 hi = 1024 262.7 / 243.8;
+# Qwen B = 1024 fp16 hi = 2048 110.3 / 98.0, fp8 hi = 1024 52.8 / 51.5),
+# while at g = 4 the flat split wins at fp16 hi = 2048.
 UNSPLIT_SHORT_MAX_TOKENS = {"fp16": 1024, "bf16": 1024, "fp8_e5m2": 256}
 UNSPLIT_RAGGED_MAX_TOKENS = {"fp16": 1024, "bf16": 1024, "fp8_e5m2": 512}
 RAGGED_UNSPLIT_MIN_WGS_PER_CU = 8
+WIDE_GROUP_MIN = 7
 UNSPLIT_MAX_KV_BYTES = {"fp16": 512 << 20, "bf16": 512 << 20, "fp8_e5m2": 192 << 20,
                         "int8": 96 << 20}
 # Every flat wave and every merge wave scans seq_lens (512 lengths per round
@@ -154,15 +162,17 @@ def short_batch_runs_unsplit(batch: int, max_seq_len: int, num_kv_heads: int, gr
     UNSPLIT_SHORT_MAX_TOKENS; any batch with RAGGED_UNSPLIT_MIN_WGS_PER_CU
     unsplit workgroups per CU up to UNSPLIT_RAGGED_MAX_TOKENS. Needs only the
     batch size and the longest length, so a caller without the lengths (the
-    vLLM boundary) applies the ragged rule.
+    vLLM boundary) applies the ragged rule. Groups of WIDE_GROUP_MIN or more
+    q heads per kv head double both limits.
     """
     if max_seq_len <= 0:
         return False
-    if uniform and max_seq_len <= UNSPLIT_SHORT_MAX_TOKENS.get(kv_dtype, 0):
+    wide = 2 if group >= WIDE_GROUP_MIN else 1
+    if uniform and max_seq_len <= wide * UNSPLIT_SHORT_MAX_TOKENS.get(kv_dtype, 0):
         return True
     units = num_kv_heads * -(-group // _abi.PA_MAX_GROUP)
     return (batch * units >= RAGGED_UNSPLIT_MIN_WGS_PER_CU * max(1, sm_count)
-            and max_seq_len <= UNSPLIT_RAGGED_MAX_TOKENS.get(kv_dtype, 0))
+            and max_seq_len <= wide * UNSPLIT_RAGGED_MAX_TOKENS.get(kv_dtype, 0))
 
 
 def plan_num_splits(seq_lens, num_kv_heads: int, group: int, sm_count: int) -> tuple[int, int]:

@@ -483,6 +483,14 @@ def test_short_batch_runs_unsplit_thresholds():
     # twice the CUs need twice the batch
     assert not sbu(nb, 512, 8, 4, 2 * cus, "fp16")
     assert sbu(2 * nb, 512, 8, 4, 2 * cus, "fp16")
+    # groups of WIDE_GROUP_MIN or more q heads per kv head double the limits
+    from pagedattn.hip_decode import WIDE_GROUP_MIN as wg
+    for kv, lim in UNSPLIT_RAGGED_MAX_TOKENS.items():
+        assert sbu(nb, 2 * lim, 8, wg, cus, kv) and not sbu(nb, 2 * lim + 1, 8, wg, cus, kv)
+        assert not sbu(nb, 2 * lim, 8, wg - 1, cus, kv)
+    for kv, lim in UNSPLIT_SHORT_MAX_TOKENS.items():
+        assert sbu(1, 2 * lim, 8, wg, cus, kv, uniform=True)
+        assert not sbu(1, 2 * lim + 1, 8, wg, cus, kv, uniform=True)
     # a group above PA_MAX_GROUP takes two head tiles per kv head
     g2 = _abi.PA_MAX_GROUP + 1
     assert sbu(nb // 2, 512, 8, g2, cus, "fp16")
