@@ -353,28 +353,32 @@ def test_flat_ragged_batch_of_1000():
         assert torch.equal(flat[dead].float().cpu(), torch.zeros((len(dead), 32, 128)))
 
 
-@pytest.mark.parametrize("kv", ["fp16", "fp8_e5m2"])
-def test_large_batch_of_short_sequences_runs_unsplit(kv):
-    """A ragged batch of 256 sequences of 32 to 512 tokens (8 unsplit
-    workgroups per CU at 256 CUs): the planner runs it unsplit, the automatic
-    launch is bit-identical to an explicit unsplit one, and sampled rows
-    match the oracle."""
+@pytest.mark.parametrize("shape,batch,hi,kv", [
+    (LLAMA3_8B, 256, 512, "fp16"), (LLAMA3_8B, 256, 512, "fp8_e5m2"),
+    (QWEN25_05B, 1024, 1500, "fp16")], ids=["llama-fp16", "llama-fp8", "qwen-fp16-wide"])
+def test_large_batch_of_short_sequences_runs_unsplit(shape, batch, hi, kv):
+    """Ragged batches of short sequences with 8 unsplit workgroups per CU at
+    256 CUs: the planner runs them unsplit (the Qwen shape's group of 7 q
+    heads per kv head doubles the length limit, so its sequences reach 1,500
+    tokens), the automatic launch is bit-identical to an explicit unsplit
+    one, and sampled rows match the oracle."""
     from helpers import subset_cache
-    from pagedattn import plan_decode
+    from pagedattn import flat_waves_per_simd, plan_decode
     from pagedattn.hip_decode import _cu_count
 
     g = torch.Generator().manual_seed(47)
-    lens = torch.randint(32, 513, (256,), generator=g).tolist()
-    c = allocate(LLAMA3_8B, len(lens), lens, seed=47, device="cuda", fill_device="cuda", kv_dtype=kv)
-    q = seeded_q(len(lens), 32, 128, 47, device="cuda")
-    planned = plan_decode(lens, 8, 4, _cu_count(q.device), 1, kv_dtype=kv, head_dim=128)
-    print(f"kv={kv} plan {planned}", flush=True)
+    lens = torch.randint(32, hi + 1, (batch,), generator=g).tolist()
+    c = allocate(shape, len(lens), lens, seed=47, device="cuda", fill_device="cuda", kv_dtype=kv)
+    q = seeded_q(len(lens), shape.num_q_heads, shape.head_dim, 47, device="cuda")
+    planned = plan_decode(lens, shape.num_kv_heads, shape.gqa_group, _cu_count(q.device),
+                          flat_waves_per_simd(kv, shape.head_dim), kv_dtype=kv, head_dim=shape.head_dim)
+    print(f"{shape.name} kv={kv} plan {planned}", flush=True)
     if planned != (1, max(lens), 0):
         pytest.skip(f"the plan {planned} on this GPU is not unsplit")
     auto = paged_decode_hip(q, c).clone()
     unsplit = paged_decode_hip(q, c, num_splits=1)
     torch.cuda.synchronize()
     assert torch.equal(auto, unsplit)
-    rows = [0, 128, 255]
+    rows = [0, batch // 2, batch - 1]
     want = oracle.reference_decode(q[rows].cpu(), subset_cache(c, rows), out_dtype=torch.float32)
     assert max_abs(auto[rows], want) < ABS_TOL
