@@ -11,9 +11,10 @@ seq_lens), then per layer:
   * writes the new token's K/V into the paged cache (`reshape_and_cache`, the
     step before the decode, integration/vllm_backend.py:117-122);
   * runs the decode with the launch the vLLM boundary would pick from the
-    batch size and the longest length (no host-side lengths, so no device
-    sync): the flat split (`flat_splits_for`), or the unsplit kernel for a
-    large batch of short sequences (`short_batch_runs_unsplit`).
+    batch size and the longest length (`plan_launch` with no host-side
+    lengths, so no device sync): the flat split, the unsplit kernel for a
+    large batch of short sequences, or the classic split for a small batch
+    (`--launch flat|unsplit` forces one).
 With --graph the whole step is captured once as a HIP graph and replayed per
 step, which is how a serving loop removes the per-launch host cost.
 
@@ -45,7 +46,7 @@ sys.path.insert(0, str(pathlib.Path(__file__).resolve().parent.parent))
 import torch  # noqa: E402
 
 from pagedattn import (LLAMA3_8B, LLAMA3_70B, QWEN25_05B, allocate, flat_splits_for,  # noqa: E402
-                       flat_waves_per_simd, short_batch_runs_unsplit)
+                       flat_waves_per_simd, plan_launch)
 from pagedattn.cache_ops import reshape_and_cache  # noqa: E402
 from pagedattn.hip_decode import _cu_count, paged_decode_hip  # noqa: E402
 
@@ -106,12 +107,17 @@ def run(args, keep_state: bool = False):
         layers.append((c, slots, q, kv, torch.empty_like(q)))
 
     wps = flat_waves_per_simd(args.kv, shape.head_dim, sdt if args.kv == "int8" else None)
+    # one launch for the whole run, planned as the vLLM boundary plans a step
+    # (batch size and the longest length the run reaches, no host lengths)
     flat = flat_splits_for(shape.num_kv_heads, shape.gqa_group, _cu_count(dev), wps)
-    # one launch for the whole run, chosen from the longest length it reaches
-    if short_batch_runs_unsplit(b, total, shape.num_kv_heads, shape.gqa_group, _cu_count(dev), args.kv):
+    mode = getattr(args, "launch", "plan")
+    if mode == "flat":
+        launch = {"flat_splits": flat}
+    elif mode == "unsplit":
         launch = {"num_splits": 1, "max_seq_len": total}
     else:
-        launch = {"flat_splits": flat}
+        launch = plan_launch(b, total, shape.num_kv_heads, shape.gqa_group, _cu_count(dev), wps,
+                             kv_dtype=args.kv, head_dim=shape.head_dim).launch_kwargs()
     counters = {"decode_calls": 0, "decode_tokens": 0, "delegated_calls": 0}
 
     def step(s: int) -> None:
@@ -184,7 +190,7 @@ def run(args, keep_state: bool = False):
     c, _, q, _, out = layers[-1]
     a = paged_decode_hip(q, c, **launch).clone()
     a2 = paged_decode_hip(q, c, **launch)
-    other = {"flat_splits": flat} if "num_splits" in launch else {"num_splits": 1}
+    other = {"flat_splits": flat} if "flat_splits" not in launch else {"num_splits": 1}
     ref = paged_decode_hip(q, c, **other)
     torch.cuda.synchronize()
     # each launch rounds its fp32 result to the fp16/bf16 output on its own,
@@ -238,6 +244,8 @@ def main() -> None:
     ap.add_argument("--slo", default="10,20,50,100")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--graph", action="store_true", help="replay each step as one HIP graph")
+    ap.add_argument("--launch", default="plan", choices=["plan", "flat", "unsplit"],
+                    help="plan: as the vLLM boundary plans the step (default); or force one launch")
     ap.add_argument("--out", default=None, help="append the run to this JSON file ({'runs': [...]})")
     args = ap.parse_args()
     if args.output_tokens < 1 or args.prompt < 1 or args.requests < 1 or args.layers < 1:

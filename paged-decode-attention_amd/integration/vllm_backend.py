@@ -9,14 +9,21 @@ routing rule (`vllm_backend.py:67-149`):
     pure decode (max_query_len == 1), fp16, supported shape -> HIP kernel
     anything else                                          -> super().forward()
 
-The backend subclasses vLLM's Triton backend, so vLLM keeps building the
-metadata (slot mapping, block tables, seq_lens) and the
+The backend subclasses vLLM's Triton backend (or, through
+`install(prefill_backend=...)`, another vLLM backend with the same cache
+layout, such as vLLM-ROCm's AITER flash-attention backend, which then serves
+prefill and mixed batches), so vLLM keeps building the metadata (slot
+mapping, block tables, seq_lens) and the
 [2, num_blocks, block_size, num_kv_heads, head_size] cache; `kv_cache.unbind(0)`
 gives the NHD views the kernel reads in place.
 
 Differences from the reference:
   * bf16 caches are served as the reference serves them (vllm_backend.py:132):
     rows converted to fp16 in registers (round to nearest even), q/out bf16.
+  * `install(prefill_backend=...)` / PAGEDATTN_PREFILL_BACKEND choose the base
+    backend that serves prefill and mixed batches (`BASE_BACKENDS`).
+  * The launch is planned by `pagedattn.plan_launch`, the planner the decode
+    wrapper itself uses, from the step's size and longest length.
   * The classes are built by `build_backend_classes(base_backend, base_impl)`,
     so the routing is testable with stand-in base classes where vLLM is not
     installed; `install(platform_cls=...)` likewise accepts a stand-in platform.
@@ -40,19 +47,14 @@ if str(_PKG_ROOT) not in sys.path:
 
 from pagedattn.cache import PagedKVCache  # noqa: E402
 from pagedattn.config import ModelShape  # noqa: E402
-from pagedattn.hip_decode import (  # noqa: E402
-    FLAT_MAX_BATCH,
-    MIN_FLAT_TILES_PER_WAVE,
-    SINGLE_SEQ_SPLIT_MAX_TOKENS,
-    TILE_TOKENS,
-    flat_splits_for,
-    flat_waves_per_simd,
-    short_batch_runs_unsplit,
-)
+from pagedattn.hip_decode import flat_waves_per_simd, plan_launch  # noqa: E402
 from pagedattn.triton_decode import paged_decode_triton, pick_num_splits  # noqa: E402
 
 QUALNAME = "integration.vllm_backend.PagedAttnTritonBackend"
-BACKEND_NAME = "PAGEDATTN_HIP"
+# The reference backend's registered name (vllm_backend.py:154-156), kept so
+# that logs, configs and tooling keyed on it see the same backend; the
+# kernels underneath are the HIP ones.
+BACKEND_NAME = "PAGEDATTN_TRITON"
 SUPPORTED_HEAD_DIMS = (32, 64, 128, 256)
 
 # Proof that the kernel ran (vllm_backend.py:64): decode calls, decoded
@@ -142,6 +144,15 @@ def _cu_count(device: torch.device) -> int:
     return _CU_COUNT[idx]
 
 
+def _host_seq_lens(attn_metadata, n: int):
+    """The step's lengths as host ints when the metadata holds a CPU copy
+    (`seq_lens_cpu`, as newer vLLM common metadata does), else None."""
+    t = getattr(attn_metadata, "seq_lens_cpu", None)
+    if isinstance(t, torch.Tensor) and t.device.type == "cpu":
+        return t[:n].tolist()
+    return None
+
+
 def decode_forward(impl, layer, query, key, value, kv_cache, attn_metadata, output,
                    write_kv: Callable = _write_kv, decode: Callable = paged_decode_triton):
     """The decode half of `forward` (vllm_backend.py:113-149): write K/V, view
@@ -161,33 +172,26 @@ def decode_forward(impl, layer, query, key, value, kv_cache, attn_metadata, outp
         block_table=attn_metadata.block_table[:n],
         seq_lens=attn_metadata.seq_lens[:n],
     )
-    # Host-side only (no device sync): max_seq_len is a host int in the
-    # metadata. The flat split needs no lengths; it is taken when the batch
-    # can hold enough tiles for its waves (the upper bound
-    # n * ceil(max_seq_len / 32) against plan_decode's threshold) and is not
-    # a large batch of short sequences (plan_decode's ragged rule, which
-    # needs only n and max_seq_len), otherwise the classic split, chunked
-    # from the longest sequence.
+    # Planned on the host with no device sync: the step's size and longest
+    # length are host ints in the metadata. Metadata that also carries the
+    # lengths on the host (`seq_lens_cpu`) gives the planner the whole batch,
+    # the same input `paged_decode_hip(num_splits=None)` plans from;
+    # otherwise it plans for a ragged batch of up to max_seq_len tokens.
     msl = int(attn_metadata.max_seq_len)
-    group = impl.num_heads // impl.num_kv_heads
-    cus = _cu_count(query.device)
-    flat = flat_splits_for(impl.num_kv_heads, group, cus, flat_waves_per_simd(cache.kv_dtype, impl.head_size))
-    single = n == 1 and msl <= SINGLE_SEQ_SPLIT_MAX_TOKENS  # plan_decode's single-sequence rule
-    short = short_batch_runs_unsplit(n, msl, impl.num_kv_heads, group, cus, cache.kv_dtype)
-    if (not single and not short and n <= FLAT_MAX_BATCH
-            and n * -(-msl // TILE_TOKENS) >= MIN_FLAT_TILES_PER_WAVE * flat):
-        decode(query[:n], cache, out=output[:n], sm_scale=impl.scale, flat_splits=flat)
-    else:
-        splits = pick_num_splits(n, impl.num_kv_heads, msl, cus)
-        decode(query[:n], cache, out=output[:n], num_splits=splits, sm_scale=impl.scale,
-               max_seq_len=msl)
+    plan = plan_launch(n, msl, impl.num_kv_heads, impl.num_heads // impl.num_kv_heads,
+                       _cu_count(query.device), flat_waves_per_simd(cache.kv_dtype, impl.head_size),
+                       kv_dtype=cache.kv_dtype, head_dim=impl.head_size,
+                       seq_lens=_host_seq_lens(attn_metadata, n))
+    decode(query[:n], cache, out=output[:n], sm_scale=impl.scale, **plan.launch_kwargs())
     STATS["decode_calls"] += 1
     STATS["decode_tokens"] += n
     return output
 
 
 def build_backend_classes(base_backend: type, base_impl: type) -> tuple[type, type]:
-    """The (backend, impl) pair on top of vLLM's Triton backend classes."""
+    """The (backend, impl) pair on top of a vLLM backend's classes (its
+    metadata builder and cache layout, and its forward for everything this
+    kernel does not serve)."""
 
     class PagedAttnTritonImpl(base_impl):  # type: ignore[misc, valid-type]
         """Pure decode -> HIP kernel; everything else -> the base class."""
@@ -205,7 +209,7 @@ def build_backend_classes(base_backend: type, base_impl: type) -> tuple[type, ty
             return decode_forward(self, layer, query, key, value, kv_cache, attn_metadata, output)
 
     class PagedAttnTritonBackend(base_backend):  # type: ignore[misc, valid-type]
-        """vLLM's Triton backend (metadata, cache layout) with our impl."""
+        """The base backend (metadata, cache layout) with our impl."""
 
         @staticmethod
         def get_name() -> str:
@@ -218,29 +222,118 @@ def build_backend_classes(base_backend: type, base_impl: type) -> tuple[type, ty
     return PagedAttnTritonBackend, PagedAttnTritonImpl
 
 
-try:  # vLLM is optional: the module imports (and is testable) without it
-    from vllm.v1.attention.backends.triton_attn import TritonAttentionBackend, TritonAttentionImpl
+# Base classes the backend can be built on. Prefill, mixed batches and every
+# delegated case run the base class's `forward`, so the base decides their
+# speed: the reference inherits vLLM's Triton backend and lost 1.9x on
+# prefill that way (README.md:186; integration/vllm_backend.py:93-111).
+# Each base must keep the NHD cache the decode reads in place,
+# [2, num_blocks, block_size, num_kv_heads, head_size] (checked through its
+# get_kv_cache_shape when the classes are built).
+#   triton         vLLM's Triton backend: the reference's base, the default
+#   rocm_aiter_fa  vLLM-ROCm's AITER flash-attention backend (CK kernels for
+#                  prefill on MI300/MI355); needs the `aiter` package
+#   flash_attn     vLLM's FlashAttention backend
+#   auto           rocm_aiter_fa where it and `aiter` import, else triton
+# A "module:BackendClass:ImplClass" string names any other base.
+BASE_BACKENDS: dict[str, tuple[str, str, str]] = {
+    "triton": ("vllm.v1.attention.backends.triton_attn", "TritonAttentionBackend",
+               "TritonAttentionImpl"),
+    "rocm_aiter_fa": ("vllm.v1.attention.backends.rocm_aiter_fa", "AiterFlashAttentionBackend",
+                      "AiterFlashAttentionImpl"),
+    "flash_attn": ("vllm.v1.attention.backends.flash_attn", "FlashAttentionBackend",
+                   "FlashAttentionImpl"),
+}
+DEFAULT_BASE = "triton"
+# The base the module-level classes are built on (None without vLLM).
+BASE_NAME: str | None = None
 
+
+def _import_base(spec: str) -> tuple[type, type]:
+    """(backend class, impl class) of a BASE_BACKENDS key or a
+    "module:BackendClass:ImplClass" string."""
+    import importlib
+
+    if spec in BASE_BACKENDS:
+        mod_name, backend_name, impl_name = BASE_BACKENDS[spec]
+    else:
+        parts = spec.split(":")
+        if len(parts) != 3:
+            raise ValueError(f"unknown base backend {spec!r}: one of {sorted(BASE_BACKENDS)}, "
+                             "'auto', or 'module:BackendClass:ImplClass'")
+        mod_name, backend_name, impl_name = parts
+    mod = importlib.import_module(mod_name)
+    return getattr(mod, backend_name), getattr(mod, impl_name)
+
+
+def resolve_base(spec: str | None = None) -> tuple[str, type, type]:
+    """(name, backend class, impl class) of the base to build on. `auto`
+    prefers rocm_aiter_fa when its module and the `aiter` package import."""
+    spec = spec or DEFAULT_BASE
+    if spec == "auto":
+        import importlib
+
+        try:
+            importlib.import_module("aiter")
+            backend, impl = _import_base("rocm_aiter_fa")
+            return "rocm_aiter_fa", backend, impl
+        except Exception:
+            spec = "triton"
+    backend, impl = _import_base(spec)
+    return spec, backend, impl
+
+
+def check_nhd_layout(base_backend: type) -> None:
+    """Raise unless the base lays its cache out as [2, NB, P, H_kv, D]: the
+    decode views `kv_cache.unbind(0)` as the NHD pages it reads."""
+    get_shape = getattr(base_backend, "get_kv_cache_shape", None)
+    if get_shape is None:
+        raise ValueError(f"{base_backend.__name__} has no get_kv_cache_shape")
+    got = tuple(get_shape(3, 16, 2, 64))
+    if got != (2, 3, 16, 2, 64):
+        raise ValueError(f"{base_backend.__name__} lays its KV cache out as {got} for "
+                         "(num_blocks=3, block_size=16, num_kv_heads=2, head_size=64); the "
+                         "decode kernel reads [2, num_blocks, block_size, num_kv_heads, head_size]")
+
+
+def use_base(spec: str | None = None) -> str:
+    """Rebuild the module's PagedAttnTritonBackend / PagedAttnTritonImpl on
+    another base (`BASE_BACKENDS` key, `auto`, or a qualified pair), so that
+    QUALNAME resolves to them. Returns the base's name."""
+    global PagedAttnTritonBackend, PagedAttnTritonImpl, BASE_NAME
+    name, backend, impl = resolve_base(spec)
+    check_nhd_layout(backend)
+    PagedAttnTritonBackend, PagedAttnTritonImpl = build_backend_classes(backend, impl)
+    BASE_NAME = name
+    return name
+
+
+try:  # vLLM is optional: the module imports (and is testable) without it
+    _import_base(DEFAULT_BASE)
     HAVE_VLLM = True
 except Exception:  # pragma: no cover - depends on the environment
     HAVE_VLLM = False
 
+PagedAttnTritonBackend = None  # type: ignore[assignment]
+PagedAttnTritonImpl = None  # type: ignore[assignment]
 if HAVE_VLLM:  # pragma: no cover - needs vLLM
-    PagedAttnTritonBackend, PagedAttnTritonImpl = build_backend_classes(
-        TritonAttentionBackend, TritonAttentionImpl)
-else:
-    PagedAttnTritonBackend = None  # type: ignore[assignment]
-    PagedAttnTritonImpl = None  # type: ignore[assignment]
+    use_base(DEFAULT_BASE)
 
 
-def install(platform_cls: type | None = None) -> str:
+def install(platform_cls: type | None = None, prefill_backend: str | None = None) -> str:
     """Make vLLM pick this backend for plain (non-MLA) V1 attention.
 
     vLLM resolves the attention backend through the platform's
     `get_attn_backend_cls(...)`, which returns a qualname string; this wraps
     that classmethod once (idempotent) so the V1 non-MLA case returns
     QUALNAME (vllm_backend.py:180-205). Returns QUALNAME.
+
+    `prefill_backend` (an addition) rebuilds the classes on another vLLM
+    backend first (`use_base`): pure decode steps still run the HIP kernel,
+    prefill and mixed batches run that backend's attention. None keeps the
+    current base (vLLM's Triton backend unless changed).
     """
+    if prefill_backend is not None:
+        use_base(prefill_backend)
     if platform_cls is None:
         from vllm.platforms import current_platform
 
@@ -263,8 +356,9 @@ def install(platform_cls: type | None = None) -> str:
 
 def maybe_install_from_env(platform_cls: type | None = None) -> bool:
     """`install()` when PAGEDATTN_VLLM_BACKEND is 1/true: the hook for a
-    `vllm.general_plugins` entry point in the worker (vllm_backend.py:208-214)."""
+    `vllm.general_plugins` entry point in the worker (vllm_backend.py:208-214).
+    PAGEDATTN_PREFILL_BACKEND, when set, is passed as `prefill_backend`."""
     if os.environ.get("PAGEDATTN_VLLM_BACKEND", "") not in ("1", "true", "True"):
         return False
-    install(platform_cls)
+    install(platform_cls, os.environ.get("PAGEDATTN_PREFILL_BACKEND") or None)
     return True

@@ -8,7 +8,7 @@ the package (oracle/).
 """
 
 from .config import LLAMA3_8B, LLAMA3_70B, MHA_DEBUG, QWEN25_05B, KVDType, ModelShape, kv_bytes_per_token
-from .cache import PagedKVCache, allocate, quantize_kv
+from .cache import PagedKVCache, allocate, dequantize_kv, gather_contiguous, quantize_kv
 from .cache_ops import reshape_and_cache
 from .hip_decode import (
     decode_partials,
@@ -18,7 +18,9 @@ from .hip_decode import (
     paged_decode_hip,
     paged_decode_triton,
     pick_num_splits,
+    LaunchPlan,
     plan_decode,
+    plan_launch,
     plan_num_splits,
     short_batch_runs_unsplit,
     split_reduce,
@@ -27,8 +29,8 @@ from .hip_decode import (
 __all__ = [
     "LLAMA3_8B", "LLAMA3_70B", "MHA_DEBUG", "QWEN25_05B", "KVDType", "ModelShape",
     "kv_bytes_per_token",
-    "PagedKVCache", "allocate", "quantize_kv", "reshape_and_cache",
+    "PagedKVCache", "allocate", "gather_contiguous", "quantize_kv", "dequantize_kv", "reshape_and_cache",
     "paged_decode_hip", "paged_decode_triton", "pick_num_splits", "plan_num_splits",
-    "plan_decode", "short_batch_runs_unsplit", "flat_needs_merge", "flat_splits_for", "flat_waves_per_simd",
+    "plan_decode", "plan_launch", "LaunchPlan", "short_batch_runs_unsplit", "flat_needs_merge", "flat_splits_for", "flat_waves_per_simd",
     "decode_partials", "split_reduce",
 ]

@@ -59,6 +59,30 @@ def quantize_kv(
     raise ValueError(f"unknown kv_dtype {kv_dtype}")
 
 
+def dequantize_kv(
+    q: torch.Tensor, scale: torch.Tensor | None, kv_dtype: KVDType
+) -> torch.Tensor:
+    """Stored cache rows -> fp16, the values the decode kernel attends over.
+
+    The reference's `dequantize_kv` (cache.py:51-62): fp16 / bf16 / fp8_e5m2
+    are casts to fp16 (e5m2 -> fp16 is exact, bf16 -> fp16 rounds to nearest
+    even). int8 is `fp16(x * scale)` with one scale per (token, head), i.e.
+    `scale` has q's shape without the last (head_dim) axis. The product is
+    formed in fp32 and rounded once: for an fp16 scale the product of an
+    8-bit integer and an 11-bit significand is exact in fp32, so this equals
+    the reference's fp16 multiply bit for bit; for fp32 scales it is the
+    single rounding the kernel applies.
+    """
+    if kv_dtype in ("fp16", "bf16", "fp8_e5m2"):
+        return q.to(torch.float16)
+    if kv_dtype == "int8":
+        if scale is None:
+            raise ValueError("int8 rows need their per-(token, head) scales")
+        prod = q.to(torch.float32) * scale.to(torch.float32)[..., None]
+        return prod.to(torch.float16)
+    raise ValueError(f"unknown kv_dtype {kv_dtype}")
+
+
 @dataclasses.dataclass
 class PagedKVCache:
     """The reference's cache dataclass (cache.py:70-102), same field names."""
@@ -201,3 +225,39 @@ def allocate(
         block_table=block_table.to(device),
         seq_lens=seq_lens_t.to(device),
     )
+
+
+def gather_contiguous(cache: PagedKVCache) -> tuple[torch.Tensor, torch.Tensor]:
+    """The paged cache as dense [B, H_kv, S_max, D] fp16 K and V tensors.
+
+    The reference's `gather_contiguous` (cache.py:187-215), for callers that
+    need a page-free view (dense attention baselines, debugging, the oracle's
+    own restatement). It runs on the cache's device with torch indexing and
+    is not part of the decode path: the HIP kernels read the pages in place.
+
+    Position s of sequence b reads page `block_table[b, s // P]` at row
+    `s % P`, dequantised with `dequantize_kv`. Positions at or past T_b hold
+    whatever their page-table entry points at: the column index is clamped
+    to the last column of the block table and unused entries are 0, as in
+    the reference, so callers mask them by `seq_lens`.
+    """
+    bt = cache.block_table
+    b = int(bt.shape[0])
+    h, d = cache.shape.num_kv_heads, cache.shape.head_dim
+    dev = cache.k_cache.device
+    s_max = int(cache.seq_lens.max().item()) if b else 0
+    if b == 0 or s_max <= 0:
+        empty = torch.empty((b, h, 0, d), dtype=torch.float16, device=dev)
+        return empty, empty.clone()
+    page = cache.block_size
+    pos = torch.arange(s_max, device=bt.device)
+    col = torch.clamp(pos // page, max=int(bt.shape[1]) - 1)
+    blocks = bt.index_select(1, col).to(dev, torch.long)        # [B, S] physical block
+    rows = (pos % page).to(dev).unsqueeze(0).expand(b, s_max)  # [B, S] row in the page
+
+    def dense(rows_t: torch.Tensor, scale_t: torch.Tensor | None) -> torch.Tensor:
+        vals = rows_t[blocks, rows]                            # [B, S, H, D] stored dtype
+        sc = None if scale_t is None else scale_t[blocks, rows]  # [B, S, H]
+        return dequantize_kv(vals, sc, cache.kv_dtype).transpose(1, 2).contiguous()
+
+    return dense(cache.k_cache, cache.k_scale), dense(cache.v_cache, cache.v_scale)

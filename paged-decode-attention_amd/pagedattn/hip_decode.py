@@ -17,6 +17,7 @@ the page size; split ranges are aligned to the kernels' 32-token tile.
 from __future__ import annotations
 
 import ctypes
+import dataclasses
 import threading
 
 import torch
@@ -29,21 +30,29 @@ from .cache import PagedKVCache
 WAVES_PER_WORKGROUP = 4
 TILE_TOKENS = 32
 SIMDS_PER_CU = 4
+
+# The launch planner's thresholds. Lengths are counted in 32-token tiles (the
+# unit every kernel streams and the flat split deals out), batch sizes in
+# workgroups or waves per CU, and cache sizes in K/V bytes per CU, so the
+# rules scale with the CU count of the device. The values were measured on a
+# 256-CU MI355X (graph-timed whole calls); the measurements are quoted at
+# each constant.
+
 # The classic split serves the batches too small for the flat split, which
 # are latency-bound: it is sized for one round of one workgroup per CU, with
-# chunks of at least MIN_SPLIT_TOKENS (2 tiles). Graph-timed whole calls at
-# the Llama-3-8B shape, this rule against the previous one (two rounds of two
+# chunks of at least MIN_SPLIT_TILES. Graph-timed whole calls at the
+# Llama-3-8B shape, this rule against the previous one (two rounds of two
 # workgroups per CU, chunks of at least 512 tokens): B = 1, T = 2048 9.6 /
 # 12.3 us; B = 1, T = 8192 13.1 / 14.5; B = 4, T = 512 8.7 / 9.5; B = 4,
 # T = 2048 12.4 / 13.5.
-MIN_SPLIT_TOKENS = 64
+MIN_SPLIT_TILES = 2
 # Sequences this short are never split: the merge launch costs more than the
 # split saves (C1, T <= 192: 4.5 us unsplit, 6.9 with 2-3 splits).
-UNSPLIT_MAX_TOKENS = 256
+UNSPLIT_MAX_TILES = 8
 # A ragged batch with a workgroup for every CU is split only when its longest
 # sequence exceeds this (B = 32, T <= 512: 11.0 us unsplit, 14.9 with 2
 # splits, 22.6 with 8).
-RAGGED_SPLIT_MIN_TOKENS = 1024
+RAGGED_SPLIT_MIN_TILES = 32
 
 # Flat split: one round of waves, at most FLAT_WAVES_PER_SIMD per SIMD even
 # where the registers allow more. One streaming wave per SIMD measured
@@ -54,26 +63,28 @@ RAGGED_SPLIT_MIN_TOKENS = 1024
 # 32-token tiles; smaller batches are latency-bound and run faster unsplit.
 FLAT_WAVES_PER_SIMD = 1
 MIN_FLAT_TILES_PER_WAVE = 4
-# A single sequence up to this length takes the classic split: cut into one
-# chunk per CU it merges 32 partials per head, the flat split 128 (graph-
+# A single sequence up to this many tiles takes the classic split: cut into
+# one chunk per CU it merges 32 partials per head, the flat split 128 (graph-
 # timed whole calls, classic against flat: T = 16384 17.9 / 21.0 us, 32768
 # 27.6 / 30.6, 65536 47.2 / 49.6; at 131072 the flat split wins, 87.9 against
 # 91.4 with 64 splits).
-SINGLE_SEQ_SPLIT_MAX_TOKENS = 65536
-# A nearly uniform batch that fills the CUs unsplit (plan_num_splits gives
-# 1) runs unsplit while its K/V is at most this many bytes: the flat pass
-# streams faster but adds its merge launch (about 4 us). Whole-call
+SINGLE_SEQ_SPLIT_MAX_TILES = 2048
+# A nearly uniform batch that fills the CUs unsplit (one workgroup per CU or
+# more) runs unsplit while its K/V is at most this many bytes per CU: the
+# flat pass streams faster but adds its merge launch (about 4 us). Whole-call
 # break-even measured at the Llama-3-8B shape (B = 64, g = 4, D = 128, 256
 # CUs), unsplit against flat: 2-byte KV 44.4 / 46.9 us at 268 MB, 85.2 / 85.1
 # at 537 MB, 166 / 162 at 1074 MB; fp8 26.6 / 29.0 at 134 MB, 49.5 / 47.2 at
 # 268 MB; int8 18.2 / 19.5 at 67 MB, 24.5 / 24.6 at 101 MB, 31.4 / 29.6 at
-# 134 MB.
+# 134 MB. (At 256 CUs: 512 MB, 192 MB and 96 MB.)
+UNSPLIT_MAX_KV_BYTES_PER_CU = {"fp16": 2 << 20, "bf16": 2 << 20, "fp8_e5m2": 768 << 10,
+                               "int8": 384 << 10}
 # Batches of short sequences that fill the CUs run unsplit, whatever their
 # size and merge or not: the flat split loses there, because its waves
 # switch sequences every few tiles. Per KV type, the longest sequence of a
-# nearly uniform batch (UNSPLIT_SHORT_MAX_TOKENS), or of a ragged batch with
+# nearly uniform batch (UNSPLIT_SHORT_MAX_TILES), or of a ragged batch with
 # at least RAGGED_UNSPLIT_MIN_WGS_PER_CU unsplit workgroups per CU
-# (UNSPLIT_RAGGED_MAX_TOKENS). Graph-timed whole calls at the Llama-3-8B
+# (UNSPLIT_RAGGED_MAX_TILES). Graph-timed whole calls at the Llama-3-8B
 # shape (g = 4, D = 128, 256 CUs), flat against unsplit, in us:
 #   fp16 uniform: B = 128, T = 256 29.0 / 26.1, T = 1024 90.1 / 87.6, T = 2048
 #     170.8 / 170.8; B = 1024, T = 256 208.9 / 189.2, T = 1024 700.4 / 689.9,
@@ -94,12 +105,10 @@ SINGLE_SEQ_SPLIT_MAX_TOKENS = 65536
 # 70B B = 1024 fp16 hi = 2048 777.9 / 747.2, fp8 hi = 1024 262.7 / 243.8;
 # Qwen B = 1024 fp16 hi = 2048 110.3 / 98.0, fp8 hi = 1024 52.8 / 51.5),
 # while at g = 4 the flat split wins at fp16 hi = 2048.
-UNSPLIT_SHORT_MAX_TOKENS = {"fp16": 1024, "bf16": 1024, "fp8_e5m2": 256}
-UNSPLIT_RAGGED_MAX_TOKENS = {"fp16": 1024, "bf16": 1024, "fp8_e5m2": 512}
+UNSPLIT_SHORT_MAX_TILES = {"fp16": 32, "bf16": 32, "fp8_e5m2": 8}
+UNSPLIT_RAGGED_MAX_TILES = {"fp16": 32, "bf16": 32, "fp8_e5m2": 16}
 RAGGED_UNSPLIT_MIN_WGS_PER_CU = 8
 WIDE_GROUP_MIN = 7
-UNSPLIT_MAX_KV_BYTES = {"fp16": 512 << 20, "bf16": 512 << 20, "fp8_e5m2": 192 << 20,
-                        "int8": 96 << 20}
 # Every flat wave and every merge wave scans seq_lens (512 lengths per round
 # trip), so the merge grows with the batch: above this batch the classic
 # kernel runs unsplit instead. Whole calls on ragged batches (T ~ U[256,
@@ -119,6 +128,16 @@ _STORE_DTYPE = {"fp16": torch.float16, "fp8_e5m2": torch.float8_e5m2, "int8": to
                 "bf16": torch.bfloat16}
 _IO_CODE = {torch.float16: _abi.PA_IO_FP16, torch.bfloat16: _abi.PA_IO_BF16}
 _SCALE_CODE = {torch.float16: _abi.PA_SCALE_FP16, torch.float32: _abi.PA_SCALE_FP32}
+_KV_ELEM_BYTES = {"fp16": 2, "bf16": 2, "fp8_e5m2": 1, "int8": 1}
+
+
+def _tiles(tokens: int) -> int:
+    return -(-max(0, int(tokens)) // TILE_TOKENS)
+
+
+def _units(num_kv_heads: int, group: int) -> int:
+    """Workgroups of the unsplit kernel per sequence ((kv head, head tile) pairs)."""
+    return num_kv_heads * -(-group // _abi.PA_MAX_GROUP)
 
 
 def pick_num_splits(
@@ -128,29 +147,30 @@ def pick_num_splits(
 
     Same signature as the reference (triton_decode.py:248-263), MI355X policy
     from measurements:
-      * batch*kv_heads >= CUs (every CU already has a workgroup) or
-        max_seq_len <= UNSPLIT_MAX_TOKENS: no split;
+      * batch*kv_heads >= CUs (every CU already has a workgroup) or the
+        longest sequence has at most UNSPLIT_MAX_TILES tiles: no split;
       * otherwise enough splits for one workgroup per CU, but never chunks
-        below MIN_SPLIT_TOKENS tokens; no power-of-two rounding and no cap
+        below MIN_SPLIT_TILES tiles; no power-of-two rounding and no cap
         of 64.
     `block_n` is accepted for signature compatibility.
     """
     del block_n
     base = max(1, batch * num_kv_heads)
-    if base >= max(1, sm_count) or max_seq_len <= UNSPLIT_MAX_TOKENS:
+    if base >= max(1, sm_count) or _tiles(max_seq_len) <= UNSPLIT_MAX_TILES:
         return 1
     want = -(-max(1, sm_count) // base)
-    max_useful = max(1, max_seq_len // MIN_SPLIT_TOKENS)
+    max_useful = max(1, max_seq_len // (MIN_SPLIT_TILES * TILE_TOKENS))
     return int(max(1, min(want, max_useful, _abi.PA_MAX_SPLITS)))
 
 
+def _nearly_uniform(lens: list[int]) -> bool:
+    """Longest length at most 1.25 x the mean (a non-empty batch)."""
+    return bool(lens) and max(lens) > 0 and max(lens) <= 1.25 * sum(lens) / len(lens)
+
+
 def _fills_unsplit(lens: list[int], num_kv_heads: int, group: int, sm_count: int) -> bool:
-    """A nearly uniform batch (longest <= 1.25 x mean) whose unsplit
-    workgroups already give every CU one."""
-    if not lens or max(lens) == 0:
-        return False
-    units = num_kv_heads * -(-group // _abi.PA_MAX_GROUP)
-    return len(lens) * units >= max(1, sm_count) and max(lens) <= 1.25 * sum(lens) / len(lens)
+    """A nearly uniform batch whose unsplit workgroups already give every CU one."""
+    return _nearly_uniform(lens) and len(lens) * _units(num_kv_heads, group) >= max(1, sm_count)
 
 
 def short_batch_runs_unsplit(batch: int, max_seq_len: int, num_kv_heads: int, group: int,
@@ -159,58 +179,57 @@ def short_batch_runs_unsplit(batch: int, max_seq_len: int, num_kv_heads: int, gr
 
     With `uniform` (a nearly uniform batch whose unsplit workgroups give every
     CU one, `_fills_unsplit`) the longest sequence may have up to
-    UNSPLIT_SHORT_MAX_TOKENS; any batch with RAGGED_UNSPLIT_MIN_WGS_PER_CU
-    unsplit workgroups per CU up to UNSPLIT_RAGGED_MAX_TOKENS. Needs only the
-    batch size and the longest length, so a caller without the lengths (the
-    vLLM boundary) applies the ragged rule. Groups of WIDE_GROUP_MIN or more
-    q heads per kv head double both limits.
+    UNSPLIT_SHORT_MAX_TILES tiles; any batch with
+    RAGGED_UNSPLIT_MIN_WGS_PER_CU unsplit workgroups per CU up to
+    UNSPLIT_RAGGED_MAX_TILES. Needs only the batch size and the longest
+    length, so a caller without the lengths applies the ragged rule. Groups
+    of WIDE_GROUP_MIN or more q heads per kv head double both limits.
     """
     if max_seq_len <= 0:
         return False
     wide = 2 if group >= WIDE_GROUP_MIN else 1
-    if uniform and max_seq_len <= wide * UNSPLIT_SHORT_MAX_TOKENS.get(kv_dtype, 0):
+    tiles = _tiles(max_seq_len)
+    if uniform and tiles <= wide * UNSPLIT_SHORT_MAX_TILES.get(kv_dtype, 0):
         return True
-    units = num_kv_heads * -(-group // _abi.PA_MAX_GROUP)
-    return (batch * units >= RAGGED_UNSPLIT_MIN_WGS_PER_CU * max(1, sm_count)
-            and max_seq_len <= wide * UNSPLIT_RAGGED_MAX_TOKENS.get(kv_dtype, 0))
+    return (batch * _units(num_kv_heads, group) >= RAGGED_UNSPLIT_MIN_WGS_PER_CU * max(1, sm_count)
+            and tiles <= wide * UNSPLIT_RAGGED_MAX_TILES.get(kv_dtype, 0))
 
 
 def plan_num_splits(seq_lens, num_kv_heads: int, group: int, sm_count: int) -> tuple[int, int]:
-    """(num_splits, max_seq_len) for a batch whose lengths the host knows.
+    """(num_splits, max_seq_len) of the classic split for a batch whose lengths the host knows.
 
     `pick_num_splits` sees only the longest length, so it cannot tell a
     uniform batch (best unsplit when it already fills the CUs) from a ragged
     one (whose long sequences then run alone at the end). With the lengths:
       * nearly uniform (longest <= 1.25 x mean) with a workgroup for every
-        CU, or no sequence longer than UNSPLIT_MAX_TOKENS: no split;
+        CU, or no sequence longer than UNSPLIT_MAX_TILES tiles: no split;
       * batches with fewer workgroups than CUs: the balanced chunking (every
         sequence cut with the longest one's chunk) with one workgroup of
         work per CU, chunk ~ sum(T) * heads / CUs (twice that for a ragged
-        batch), at least MIN_SPLIT_TOKENS;
+        batch), at least MIN_SPLIT_TILES tiles;
       * ragged batches with a workgroup for every CU: unsplit up to
-        RAGGED_SPLIT_MIN_TOKENS, else about four rounds of workgroups,
+        RAGGED_SPLIT_MIN_TILES tiles, else about four rounds of workgroups,
         chunk ~ sum(T) * heads / (4 CUs).
     """
     lens = [max(0, int(t)) for t in seq_lens]
     if not lens or max(lens) == 0:
         return 1, 0
     tmax = max(lens)
-    units = num_kv_heads * -(-group // _abi.PA_MAX_GROUP)
-    uniform = tmax <= 1.25 * sum(lens) / len(lens)
-    if _fills_unsplit(lens, num_kv_heads, group, sm_count) or tmax <= UNSPLIT_MAX_TOKENS:
+    units = _units(num_kv_heads, group)
+    if _fills_unsplit(lens, num_kv_heads, group, sm_count) or _tiles(tmax) <= UNSPLIT_MAX_TILES:
         return 1, tmax
     work, cus = sum(lens) * units, max(1, sm_count)
     if len(lens) * units >= cus:
         # every CU has a workgroup already (a ragged batch): split only long
         # sequences, into several rounds of workgroups
-        if tmax <= RAGGED_SPLIT_MIN_TOKENS:
+        if _tiles(tmax) <= RAGGED_SPLIT_MIN_TILES:
             return 1, tmax
         chunk = work // (4 * cus)
     else:
         # one workgroup of work per CU; a ragged batch's chunks twice as long
         # (its short sequences add partly filled ones)
-        chunk = (1 if uniform else 2) * work // cus
-    chunk = max(MIN_SPLIT_TOKENS, chunk)
+        chunk = (1 if _nearly_uniform(lens) else 2) * work // cus
+    chunk = max(MIN_SPLIT_TILES * TILE_TOKENS, chunk)
     splits = max(1, min(-(-tmax // chunk), _abi.PA_MAX_SPLITS))
     return int(splits), tmax
 
@@ -219,47 +238,99 @@ def flat_splits_for(num_kv_heads: int, group: int, sm_count: int, waves_per_simd
     """One round of waves over the (kv head, head tile) units: as many as
     the CUs hold (4 SIMDs each, `waves_per_simd` waves per SIMD), capped at
     FLAT_WAVES_PER_SIMD per SIMD."""
-    units = num_kv_heads * -(-group // _abi.PA_MAX_GROUP)
     per_simd = max(1, min(waves_per_simd, FLAT_WAVES_PER_SIMD))
     waves = max(1, sm_count) * SIMDS_PER_CU * per_simd
-    return int(max(1, min(waves // units, _abi.PA_MAX_FLAT_SPLITS)))
+    return int(max(1, min(waves // _units(num_kv_heads, group), _abi.PA_MAX_FLAT_SPLITS)))
+
+
+@dataclasses.dataclass(frozen=True)
+class LaunchPlan:
+    """How one decode call is launched.
+
+    flat_splits > 0: the flat split with that many ranges per unit; `merge`
+    says whether its merge pass has work (False when every sequence lies
+    inside one range, so the decode pass writes all of `out`).
+    flat_splits == 0: the classic kernel with `num_splits` per-sequence
+    splits (1 = unsplit), chunked from `max_seq_len`.
+    """
+
+    num_splits: int
+    max_seq_len: int
+    flat_splits: int
+    merge: bool = True
+
+    def launch_kwargs(self) -> dict:
+        """Keywords of `paged_decode_hip` that select this launch."""
+        if self.flat_splits:
+            return {"flat_splits": self.flat_splits}
+        return {"num_splits": self.num_splits, "max_seq_len": self.max_seq_len}
+
+
+def plan_launch(batch: int, max_seq_len: int, num_kv_heads: int, group: int, sm_count: int,
+                waves_per_simd: int = 1, kv_dtype: str | None = None,
+                head_dim: int | None = None, seq_lens=None) -> LaunchPlan:
+    """The launch planner: every caller (the decode wrapper with
+    `num_splits=None`, the vLLM boundary, the benchmarks) plans here.
+
+    `seq_lens` (host ints) when the caller knows the lengths, else None: then
+    only `batch` and `max_seq_len` are known (a serving step's metadata,
+    which holds the lengths on the device only), and the planner assumes
+    a ragged batch whose every sequence may be that long. Rules, in order:
+      * the flat split (one round of waves, `flat_splits_for`) when each of
+        its waves gets at least MIN_FLAT_TILES_PER_WAVE tiles, the batch is
+        at most FLAT_MAX_BATCH and is not a single sequence of up to
+        SINGLE_SEQ_SPLIT_MAX_TILES tiles; with `kv_dtype` and `head_dim`
+        given, two exceptions run unsplit instead:
+          - a batch of short sequences that fills the CUs
+            (`short_batch_runs_unsplit`; the nearly-uniform limit only with
+            known lengths);
+          - a nearly uniform batch (known lengths) that fills the CUs
+            unsplit, with at most UNSPLIT_MAX_KV_BYTES_PER_CU x CUs of K/V,
+            unless the flat split needs no merge either (`flat_needs_merge`);
+      * otherwise the classic split (`plan_num_splits`), on the known
+        lengths or on `batch` sequences of `max_seq_len` tokens.
+    """
+    cus = max(1, sm_count)
+    known = seq_lens is not None
+    lens = [max(0, int(t)) for t in seq_lens] if known else None
+    if known:
+        batch = len(lens)
+        tmax = max(lens) if lens else 0
+        tiles = sum(_tiles(t) for t in lens)
+    else:
+        tmax = max(0, int(max_seq_len))
+        tiles = batch * _tiles(tmax)  # an upper bound
+    flat = flat_splits_for(num_kv_heads, group, cus, waves_per_simd)
+    flat_ok = (batch <= FLAT_MAX_BATCH and tiles >= MIN_FLAT_TILES_PER_WAVE * flat
+               and not (batch == 1 and _tiles(tmax) <= SINGLE_SEQ_SPLIT_MAX_TILES))
+    if flat_ok:
+        fills = known and _fills_unsplit(lens, num_kv_heads, group, cus)
+        merge = flat_needs_merge(lens, flat) if known else True
+        if kv_dtype is not None and head_dim is not None:
+            if short_batch_runs_unsplit(batch, tmax, num_kv_heads, group, cus, kv_dtype,
+                                        uniform=fills):
+                return LaunchPlan(1, tmax, 0)
+            kv_bytes = sum(lens) * num_kv_heads * head_dim * _KV_ELEM_BYTES.get(kv_dtype, 2) * 2 \
+                if known else 0
+            limit = UNSPLIT_MAX_KV_BYTES_PER_CU.get(kv_dtype, 0) * cus
+            if fills and kv_bytes <= limit and merge:
+                return LaunchPlan(1, tmax, 0)
+        return LaunchPlan(1, tmax, flat, merge)
+    # the classic split, planned on the lengths (unknown: every sequence as
+    # long as the longest, which sizes the chunks for the worst case)
+    splits, tmax = plan_num_splits(lens if known else [tmax] * batch, num_kv_heads, group, cus)
+    return LaunchPlan(splits, tmax, 0)
 
 
 def plan_decode(seq_lens, num_kv_heads: int, group: int, sm_count: int,
                 waves_per_simd: int = 1, kv_dtype: str | None = None,
                 head_dim: int | None = None) -> tuple[int, int, int]:
-    """(num_splits, max_seq_len, flat_splits) for a batch whose lengths the host knows.
-
-    The flat split (one round of waves, `flat_splits_for`) whenever each of
-    its waves gets at least MIN_FLAT_TILES_PER_WAVE tiles and the batch is at
-    most FLAT_MAX_BATCH: it is balanced for any mix of lengths and measured
-    fastest on every benchmark config with a split (C2-C5). Exceptions, when `kv_dtype` and
-    `head_dim` are given: a batch of short sequences that fills the CUs runs
-    unsplit (`short_batch_runs_unsplit`); a nearly uniform batch that fills
-    the CUs unsplit stays unsplit (no merge launch) up to UNSPLIT_MAX_KV_BYTES
-    of K/V, unless the flat split needs no merge either (`flat_needs_merge`).
-    Smaller batches take `plan_num_splits`.
-    """
-    lens = [max(0, int(t)) for t in seq_lens]
-    tmax = max(lens) if lens else 0
-    flat = flat_splits_for(num_kv_heads, group, sm_count, waves_per_simd)
-    tiles = sum(-(-t // TILE_TOKENS) for t in lens)
-    fits = len(lens) <= FLAT_MAX_BATCH
-    if len(lens) == 1 and tmax <= SINGLE_SEQ_SPLIT_MAX_TOKENS:
-        fits = False  # the classic split's shorter merge wins
-    if fits and tiles >= MIN_FLAT_TILES_PER_WAVE * flat:
-        if kv_dtype is not None and head_dim is not None:
-            fills = _fills_unsplit(lens, num_kv_heads, group, sm_count)
-            if short_batch_runs_unsplit(len(lens), tmax, num_kv_heads, group, sm_count, kv_dtype,
-                                        uniform=fills):
-                return 1, tmax, 0
-            elem = 1 if kv_dtype in ("fp8_e5m2", "int8") else 2
-            kv_bytes = sum(lens) * num_kv_heads * head_dim * elem * 2
-            if fills and kv_bytes <= UNSPLIT_MAX_KV_BYTES.get(kv_dtype, 0) and flat_needs_merge(lens, flat):
-                return 1, tmax, 0
-        return 1, tmax, flat
-    splits, tmax = plan_num_splits(lens, num_kv_heads, group, sm_count)
-    return splits, tmax, 0
+    """(num_splits, max_seq_len, flat_splits) for a batch whose lengths the
+    host knows: `plan_launch` with the lengths."""
+    lens = list(seq_lens)
+    p = plan_launch(len(lens), 0, num_kv_heads, group, sm_count, waves_per_simd, kv_dtype,
+                    head_dim, seq_lens=lens)
+    return p.num_splits, p.max_seq_len, p.flat_splits
 
 
 def flat_needs_merge(seq_lens, flat_splits: int, max_tokens: int | None = None) -> bool:
@@ -275,7 +346,7 @@ def flat_needs_merge(seq_lens, flat_splits: int, max_tokens: int | None = None) 
     lens = [max(0, int(t)) for t in seq_lens]
     if max_tokens is not None:
         lens = [min(t, max_tokens) for t in lens]
-    tiles = [-(-t // TILE_TOKENS) for t in lens]
+    tiles = [_tiles(t) for t in lens]
     total = sum(tiles)
     if total == 0 or flat_splits <= 0:
         return True
@@ -293,23 +364,35 @@ class _Workspace:
 
     Grows to the largest request seen and hands out views, so repeated calls
     allocate nothing (the role of the reference's `_WS`, triton_decode.py:266-282).
+    A buffer that is outgrown is retired, never freed: a HIP graph captured
+    while it was current keeps launching into it, so it must stay valid for
+    the life of the process. Growth is at least 2x, so the retired buffers
+    together hold less than the current one. `reserve` sizes the workspace
+    before a capture.
     """
 
     def __init__(self) -> None:
         self._buf: dict[torch.device, tuple[torch.Tensor, torch.Tensor]] = {}
+        self._retired: dict[torch.device, list[tuple[torch.Tensor, torch.Tensor]]] = {}
         self._lock = threading.Lock()
+
+    def _ensure(self, n_out: int, n_lse: int, device) -> tuple[torch.Tensor, torch.Tensor]:
+        with self._lock:
+            cur = self._buf.get(device)
+            if cur is None or cur[0].numel() < n_out or cur[1].numel() < n_lse:
+                grow_out = max(n_out, 1, 2 * cur[0].numel() if cur is not None else 0)
+                grow_lse = max(n_lse, 1, 2 * cur[1].numel() if cur is not None else 0)
+                if cur is not None:
+                    self._retired.setdefault(device, []).append(cur)
+                cur = (torch.empty(grow_out, dtype=torch.float32, device=device),
+                       torch.empty(grow_lse, dtype=torch.float32, device=device))
+                self._buf[device] = cur
+            return cur
 
     def get(self, b: int, hq: int, splits: int, d: int, device) -> tuple[torch.Tensor, torch.Tensor]:
         n_out = b * hq * splits * d
         n_lse = b * hq * splits
-        with self._lock:
-            cur = self._buf.get(device)
-            if cur is None or cur[0].numel() < n_out or cur[1].numel() < n_lse:
-                cur = (
-                    torch.empty(max(n_out, 1), dtype=torch.float32, device=device),
-                    torch.empty(max(n_lse, 1), dtype=torch.float32, device=device),
-                )
-                self._buf[device] = cur
+        cur = self._ensure(n_out, n_lse, device)
         return cur[0][:n_out].view(b, hq, splits, d), cur[1][:n_lse].view(b, hq, splits)
 
     def get_flat(self, slots: int, hq: int, d: int, device) -> tuple[torch.Tensor, torch.Tensor]:
@@ -317,8 +400,58 @@ class _Workspace:
         out, lse = self.get(slots, hq, 1, d, device)
         return out.view(slots, hq, d), lse.view(slots, hq)
 
+    def reserve(self, n_out: int, n_lse: int, device) -> None:
+        self._ensure(n_out, n_lse, device)
+
+    def current(self, device) -> tuple[torch.Tensor, torch.Tensor] | None:
+        return self._buf.get(device)
+
 
 _WS = _Workspace()
+
+
+def reserve_workspace(batch: int, num_q_heads: int, head_dim: int, device,
+                      num_splits: int = 1, flat_splits: int = 0) -> None:
+    """Size the split workspace for calls up to this size before capturing
+    them in a HIP graph, so that no later call grows it (a grown workspace
+    leaves the captured graph's buffers in place, so replays stay correct;
+    reserving only avoids the extra memory). Flat splits need
+    (batch + flat_splits) slots, the classic split batch * num_splits."""
+    slots = batch + flat_splits if flat_splits else batch * max(1, num_splits)
+    dev = torch.device(device)
+    if dev.index is None:
+        dev = torch.device(dev.type, torch.cuda.current_device())
+    _WS.reserve(slots * num_q_heads * head_dim, slots * num_q_heads, dev)
+
+
+def _check_partials(device: torch.device, part_out: torch.Tensor, part_lse: torch.Tensor,
+                    b: int, hq: int, d: int, num_splits: int, flat_splits: int) -> None:
+    """Caller-supplied split workspace, checked before its pointers reach a
+    kernel: float32, on `device`, head_dim contiguous, and the exact classic
+    shapes [B, Hq, S, D] / [B, Hq, S] (split stride 1 in part_lse, which the
+    kernels assume) or at least B + F flat slots [>= B+F, Hq, D] / [>= B+F, Hq]."""
+    for name, t in (("part_out", part_out), ("part_lse", part_lse)):
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{name} must be a tensor")
+        if t.dtype != torch.float32:
+            raise ValueError(f"{name} must be float32, got {t.dtype}")
+        if t.device != device:
+            raise ValueError(f"{name} is on {t.device}, q on {device}")
+    if flat_splits > 0:
+        slots = b + flat_splits
+        if part_out.dim() != 3 or part_out.shape[0] < slots or tuple(part_out.shape[1:]) != (hq, d):
+            raise ValueError(f"flat part_out {tuple(part_out.shape)} is not [>= {slots}, {hq}, {d}]")
+        if part_lse.dim() != 2 or part_lse.shape[0] < slots or part_lse.shape[1] != hq:
+            raise ValueError(f"flat part_lse {tuple(part_lse.shape)} is not [>= {slots}, {hq}]")
+        if part_out.stride(2) != 1:
+            raise ValueError("part_out must have a contiguous head dim")
+    else:
+        if tuple(part_out.shape) != (b, hq, num_splits, d):
+            raise ValueError(f"part_out {tuple(part_out.shape)} is not {(b, hq, num_splits, d)}")
+        if tuple(part_lse.shape) != (b, hq, num_splits):
+            raise ValueError(f"part_lse {tuple(part_lse.shape)} is not {(b, hq, num_splits)}")
+        if part_out.stride(3) != 1 or part_lse.stride(2) != 1:
+            raise ValueError("part_out needs a contiguous head dim and part_lse a contiguous split dim")
 _CU_COUNT: dict[int, int] = {}
 _FLAT_WPS: dict[tuple, int] = {}
 
@@ -523,10 +656,11 @@ def paged_decode_hip(
         # the lengths come to the host in the one sync the reference also makes
         lens = cache.seq_lens.tolist()
         wps = flat_waves_per_simd(cache.kv_dtype, d, None if cache.k_scale is None else cache.k_scale.dtype)
-        num_splits, longest, flat_splits = plan_decode(lens, hkv, group, _cu_count(q.device), wps,
-                                                       kv_dtype=cache.kv_dtype, head_dim=d)
+        plan = plan_launch(b, 0, hkv, group, _cu_count(q.device), wps, kv_dtype=cache.kv_dtype,
+                           head_dim=d, seq_lens=lens)
+        num_splits, flat_splits = plan.num_splits, plan.flat_splits
         if max_seq_len is None:
-            max_seq_len = longest
+            max_seq_len = plan.max_seq_len
         if flat_splits:
             merge = flat_needs_merge(lens, flat_splits, cache.block_table.shape[1] * cache.block_size)
     num_splits = int(num_splits)
@@ -590,6 +724,7 @@ def decode_partials(
         part_lse = torch.empty((b, hq, num_splits), dtype=torch.float32, device=q.device)
     if out is None:
         out = torch.empty((b, hq, d), dtype=q.dtype, device=q.device)
+    _check_partials(q.device, part_out, part_lse, b, hq, d, num_splits, flat_splits)
     args = _fill_args(q, cache, out, num_splits, scale, part_out, part_lse, max_seq_len, flat_splits)
     lib = _abi.load()
     rc = _call(q.device, lib.pa_decode_partials, ctypes.byref(args), _stream(q.device))
@@ -612,6 +747,8 @@ def flat_merge(
     if flat_splits <= 0:
         raise ValueError("flat_merge needs flat_splits > 0")
     scale = cache.shape.softmax_scale if sm_scale is None else float(sm_scale)
+    b, hq, d = q.shape
+    _check_partials(q.device, part_out, part_lse, b, hq, d, 1, flat_splits)
     args = _fill_args(q, cache, out, 1, scale, part_out, part_lse, 0, flat_splits)
     lib = _abi.load()
     rc = _call(q.device, lib.pa_flat_merge, ctypes.byref(args), _stream(q.device))
@@ -623,15 +760,18 @@ def split_reduce(
     part_out: torch.Tensor, part_lse: torch.Tensor, out: torch.Tensor | None = None
 ) -> torch.Tensor:
     """Merge split partials into [B, H, D] fp16 or bf16 (triton_decode.py:198-240)."""
+    if part_out.dim() != 4:
+        raise ValueError(f"part_out {tuple(part_out.shape)} is not [B, H, S, D]")
     b, h, s, d = part_out.shape
-    if part_out.dtype != torch.float32 or part_lse.dtype != torch.float32:
-        raise ValueError("partials must be float32")
-    if part_out.stride(3) != 1 or tuple(part_lse.shape) != (b, h, s):
-        raise ValueError("part_out must have a contiguous head dim and part_lse shape [B, H, S]")
+    _check_partials(part_out.device, part_out, part_lse, b, h, d, s, 0)
     if out is None:
         out = torch.empty((b, h, d), dtype=torch.float16, device=part_out.device)
     if out.dtype not in _IO_CODE or out.stride(2) != 1:
         raise ValueError("out must be float16 or bfloat16 with a contiguous head dim")
+    if tuple(out.shape) != (b, h, d) or out.device != part_out.device:
+        raise ValueError(f"out {tuple(out.shape)} on {out.device} is not [{b}, {h}, {d}] on {part_out.device}")
+    if not part_out.is_cuda:
+        raise ValueError(f"part_out is on {part_out.device}: the merge kernel needs GPU tensors")
     r = _abi.PaReduceArgs()
     r.part_out = part_out.data_ptr()
     r.part_lse = part_lse.data_ptr()
@@ -663,9 +803,12 @@ __all__ = [
     "split_count_for",
     "plan_num_splits",
     "plan_decode",
+    "plan_launch",
+    "LaunchPlan",
     "flat_needs_merge",
     "flat_splits_for",
     "flat_waves_per_simd",
+    "reserve_workspace",
     "WAVES_PER_WORKGROUP",
     "TILE_TOKENS",
 ]

@@ -110,3 +110,39 @@ def test_page_moves_leave_output_bit_identical_at_full_size():
     after = paged_decode_hip(q, moved, flat_splits=flat)
     torch.cuda.synchronize()
     assert torch.equal(before, after)
+
+
+def test_c1_exact_workload_every_row():
+    """BASELINE.json configs[0] exactly as bench.py builds it (Qwen2.5-0.5B
+    shape 14q/2kv d64, B = 24, T ~ U[32, 192] with seed 0, a seeded
+    permutation of a 512-block pool, fp16, scale 1/8, no split-KV). The
+    oracle sees the whole batch here: all 24 rows within 2e-3 of the fp32
+    oracle (and the reference's relative bar), for the planner's launch and
+    an explicit num_splits=1, and two calls byte-equal. The reference's own
+    Qwen-shape case is tests/test_correctness.py:162-174."""
+    import bench
+    from pagedattn import QWEN25_05B, plan_decode
+
+    wl = bench.make_workload("c1")
+    assert (wl.batch, wl.pool_blocks, wl.kv_dtype) == (24, 512, "fp16")
+    assert min(wl.lens) >= 32 and max(wl.lens) <= 192
+    used = sum(-(-t // 16) for t in wl.lens)
+    c = allocate(QWEN25_05B, wl.batch, wl.lens, block_size=16, kv_dtype="fp16", device="cuda",
+                 seed=wl.seed, slack_blocks=wl.pool_blocks - used)
+    assert c.k_cache.shape[0] == 512
+    bt = c.block_table.cpu()
+    ids = torch.cat([bt[b, : -(-t // 16)] for b, t in enumerate(wl.lens)])
+    assert ids.unique().numel() == used and int(ids.max()) < 512  # distinct pages of the pool
+    g = torch.Generator().manual_seed(100 + wl.seed)
+    q = torch.randn((24, 14, 64), dtype=torch.float16, generator=g).cuda()
+    want = oracle.reference_decode(q.cpu(), c, out_dtype=torch.float32)
+    assert plan_decode(wl.lens, 2, 7, _cu_count(q.device), 1, kv_dtype="fp16", head_dim=64)[:3:2] == (1, 0)
+    for kw in ({}, {"num_splits": 1}):
+        a = paged_decode_hip(q, c, **kw).clone()
+        b = paged_decode_hip(q, c, **kw)
+        torch.cuda.synchronize()
+        err = max_abs(a, want)
+        rel = err / want.abs().max().item()
+        print(f"c1 {kw or 'planner'}: max_abs={err:.2e} rel={rel:.2e}", flush=True)
+        assert torch.equal(a, b), "two calls differ"
+        assert err < ABS_TOL and rel < 1e-2

@@ -34,7 +34,8 @@ def test_decode_loop_last_step_matches_the_oracle(kv, graph):
     each step (each replay) the loop synchronises and compares every layer's
     output with an eager decode of the same state, bit for bit."""
     args = argparse.Namespace(shape="qwen2.5-0.5b", layers=2, requests=5, prompt=77, output_tokens=6,
-                              warmup=2, kv=kv, slo="1,10", seed=3, out=None, graph=graph, check_each=True)
+                              warmup=2, kv=kv, slo="1,10", seed=3, out=None, graph=graph, check_each=True,
+                              launch="flat")
     print(f"kv={kv} graph={graph}", flush=True)
     r, layers, launch = bench_decode_loop.run(args, keep_state=True)
     assert "flat_splits" in launch
@@ -61,7 +62,8 @@ def test_decode_loop_of_a_large_short_batch_runs_unsplit(kv, graph):
     if _cu_count(torch.device("cuda:0")) != 256:
         pytest.skip("the batch is sized for 256 CUs")
     args = argparse.Namespace(shape="llama3-8b", layers=1, requests=256, prompt=70, output_tokens=4,
-                              warmup=1, kv=kv, slo="1,10", seed=4, out=None, graph=graph, check_each=True)
+                              warmup=1, kv=kv, slo="1,10", seed=4, out=None, graph=graph, check_each=True,
+                              launch="plan")
     print(f"kv={kv} graph={graph}", flush=True)
     r, layers, launch = bench_decode_loop.run(args, keep_state=True)
     assert launch == {"num_splits": 1, "max_seq_len": 75}

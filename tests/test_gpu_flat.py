@@ -249,6 +249,46 @@ def test_decode_in_a_hip_graph(kw):
         assert torch.equal(out, eager), f"replay with q seed {seed} differs"
 
 
+@pytest.mark.parametrize("kw", [{"flat_splits": 7}, {"num_splits": 3}])
+def test_graph_replays_after_the_workspace_grows(kw, monkeypatch):
+    """A decode captured in a HIP graph keeps the split workspace it was
+    captured with: a later, larger eager call grows the workspace (the old
+    buffers are retired, not freed), and every replay still equals the eager
+    result of the captured call, bit for bit."""
+    from pagedattn import hip_decode
+
+    _WS = hip_decode._Workspace()  # a fresh workspace, sized by this test's calls only
+    monkeypatch.setattr(hip_decode, "_WS", _WS)
+    q, c = _case(LLAMA3_8B, RAGGED, seed=18)
+    out = torch.empty_like(q)
+    paged_decode_hip(q, c, out=out, **kw)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        paged_decode_hip(q, c, out=out, **kw)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        paged_decode_hip(q, c, out=out, **kw)
+    want = paged_decode_hip(q, c, **kw).clone()
+    before = _WS.current(q.device)[0].data_ptr()
+    # a call with 8x the batch: the workspace grows
+    big_lens = RAGGED * 8
+    qb, cb = _case(LLAMA3_8B, big_lens, seed=19)
+    big = {k: (v * 8 if k == "flat_splits" else v) for k, v in kw.items()}
+    paged_decode_hip(qb, cb, **big)
+    torch.cuda.synchronize()
+    assert _WS.current(q.device)[0].data_ptr() != before, "the workspace did not grow"
+    for rep in range(3):
+        out.fill_(5.0)
+        junk = torch.randn(1 << 20, device="cuda")  # allocator churn between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        del junk
+        assert torch.equal(out, want), f"replay {rep} after the workspace grew differs"
+
+
 @pytest.mark.parametrize("kw", [{"flat_splits": 7}, {"num_splits": 3}, {"num_splits": 1}])
 def test_out_of_range_lengths_and_block_ids_are_clamped(kw):
     """The kernels' own bounds: a length past the block table reads the whole

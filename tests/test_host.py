@@ -396,8 +396,10 @@ def test_flat_splits_for_and_plan_decode():
     assert plan_decode([512] * 128, 8, 4, 256, 1, kv_dtype="int8", head_dim=128) == (1, 512, 128)
     # a batch of short sequences that fills the CUs runs unsplit at any size,
     # merge or not: nearly uniform up to UNSPLIT_SHORT_MAX_TOKENS ...
-    from pagedattn.hip_decode import (RAGGED_UNSPLIT_MIN_WGS_PER_CU, UNSPLIT_RAGGED_MAX_TOKENS,
-                                      UNSPLIT_SHORT_MAX_TOKENS)
+    from pagedattn.hip_decode import (RAGGED_UNSPLIT_MIN_WGS_PER_CU, TILE_TOKENS,
+                                      UNSPLIT_RAGGED_MAX_TILES, UNSPLIT_SHORT_MAX_TILES)
+    UNSPLIT_SHORT_MAX_TOKENS = {k: v * TILE_TOKENS for k, v in UNSPLIT_SHORT_MAX_TILES.items()}
+    UNSPLIT_RAGGED_MAX_TOKENS = {k: v * TILE_TOKENS for k, v in UNSPLIT_RAGGED_MAX_TILES.items()}
     assert plan_decode([512] * 128, 8, 4, 256, 1, kv_dtype="fp16", head_dim=128) == (1, 512, 0)
     t16, t8 = UNSPLIT_SHORT_MAX_TOKENS["fp16"], UNSPLIT_SHORT_MAX_TOKENS["fp8_e5m2"]
     assert plan_decode([t16] * 1024, 8, 4, 256, 1, kv_dtype="bf16", head_dim=128) == (1, t16, 0)
@@ -430,8 +432,9 @@ def test_flat_splits_for_and_plan_decode():
     half = 16 * MIN_FLAT_TILES_PER_WAVE * f
     assert plan_decode([half, half], 1, 1, 1, 1)[2] == f
     assert plan_decode([half, half - 32], 1, 1, 1, 1)[2] == 0
-    # a single sequence takes the classic split up to SINGLE_SEQ_SPLIT_MAX_TOKENS
-    from pagedattn.hip_decode import SINGLE_SEQ_SPLIT_MAX_TOKENS as single
+    # a single sequence takes the classic split up to SINGLE_SEQ_SPLIT_MAX_TILES
+    from pagedattn.hip_decode import SINGLE_SEQ_SPLIT_MAX_TILES
+    single = SINGLE_SEQ_SPLIT_MAX_TILES * TILE_TOKENS
     assert plan_decode([single], 8, 4, 256, 1)[2] == 0
     assert plan_decode([single + 32], 8, 4, 256, 1)[2] == 128
 
@@ -463,8 +466,11 @@ def test_short_batch_runs_unsplit_thresholds():
     workgroups-per-CU threshold scaling with the CU count, and head tiles
     (groups above PA_MAX_GROUP) counting as extra workgroups."""
     from pagedattn import short_batch_runs_unsplit as sbu
-    from pagedattn.hip_decode import (RAGGED_UNSPLIT_MIN_WGS_PER_CU, UNSPLIT_RAGGED_MAX_TOKENS,
-                                      UNSPLIT_SHORT_MAX_TOKENS, _abi)
+    from pagedattn.hip_decode import (RAGGED_UNSPLIT_MIN_WGS_PER_CU, TILE_TOKENS,
+                                      UNSPLIT_RAGGED_MAX_TILES, UNSPLIT_SHORT_MAX_TILES, _abi)
+
+    UNSPLIT_SHORT_MAX_TOKENS = {k: v * TILE_TOKENS for k, v in UNSPLIT_SHORT_MAX_TILES.items()}
+    UNSPLIT_RAGGED_MAX_TOKENS = {k: v * TILE_TOKENS for k, v in UNSPLIT_RAGGED_MAX_TILES.items()}
 
     cus = 256
     nb = RAGGED_UNSPLIT_MIN_WGS_PER_CU * cus // 8  # 8 kv heads, group 4: one unit per kv head
@@ -495,3 +501,65 @@ def test_short_batch_runs_unsplit_thresholds():
     g2 = _abi.PA_MAX_GROUP + 1
     assert sbu(nb // 2, 512, 8, g2, cus, "fp16")
     assert not sbu(nb // 2, 512, 8, 4, cus, "fp16")
+
+
+def test_public_partials_helpers_reject_bad_workspaces():
+    """decode_partials / flat_merge / split_reduce check caller-supplied
+    workspaces before any pointer reaches a kernel: dtype, device, exact
+    classic shapes, enough flat slots, the split stride of part_lse, and the
+    merge output's shape."""
+    from pagedattn import LLAMA3_8B, allocate
+    from pagedattn.hip_decode import decode_partials, flat_merge, split_reduce
+
+    c = allocate(LLAMA3_8B, 2, [40, 70], device="cpu", seed=2)
+    q = torch.zeros((2, 32, 128), dtype=torch.float16)
+    f32 = dict(dtype=torch.float32)
+    good_po, good_pl = torch.zeros((2, 32, 3, 128), **f32), torch.zeros((2, 32, 3), **f32)
+    bad = [
+        (torch.zeros((2, 32, 3, 128), dtype=torch.float16), good_pl, "float32"),
+        (torch.zeros((2, 32, 2, 128), **f32), good_pl, "part_(out|lse)"),
+        (good_po, torch.zeros((2, 32, 4), **f32), "part_lse"),
+        (good_po, torch.zeros((2, 3, 32), **f32).transpose(1, 2), "contiguous split"),
+    ]
+    for po, pl, msg in bad:
+        with pytest.raises(ValueError, match=msg):
+            decode_partials(q, c, 3, part_out=po, part_lse=pl)
+        with pytest.raises(ValueError, match=msg):
+            split_reduce(po, pl)
+    # the well-formed classic workspace passes the checks and stops at the
+    # GPU-only launch
+    with pytest.raises(ValueError, match="GPU"):
+        decode_partials(q, c, 3, part_out=good_po, part_lse=good_pl)
+    with pytest.raises(ValueError, match="GPU"):
+        split_reduce(good_po, good_pl, torch.zeros((2, 32, 128), dtype=torch.float16))
+    with pytest.raises(ValueError, match="out"):
+        split_reduce(good_po, good_pl, torch.zeros((2, 32, 64), dtype=torch.float16))
+    # flat slots: at least B + F of them
+    F = 5
+    few = (torch.zeros((2 + F - 1, 32, 128), **f32), torch.zeros((2 + F, 32), **f32))
+    for po, pl in (few, (few[1].new_zeros((2 + F, 32, 128)), few[1][:-1])):
+        with pytest.raises(ValueError, match="flat"):
+            decode_partials(q, c, 1, part_out=po, part_lse=pl, flat_splits=F)
+        with pytest.raises(ValueError, match="flat"):
+            flat_merge(q, c, F, po, pl, torch.zeros_like(q))
+    with pytest.raises(ValueError, match="float32"):
+        flat_merge(q, c, F, torch.zeros((2 + F, 32, 128), dtype=torch.float16),
+                   torch.zeros((2 + F, 32), **f32), torch.zeros_like(q))
+
+
+def test_workspace_keeps_outgrown_buffers():
+    """A grown workspace retires the old buffers instead of freeing them (a
+    captured HIP graph may still launch into them), growing at least 2x."""
+    from pagedattn.hip_decode import _Workspace
+
+    ws = _Workspace()
+    dev = torch.device("cpu")
+    a, _ = ws.get(2, 4, 1, 8, dev)
+    p0 = a.data_ptr()
+    b, _ = ws.get(2, 4, 1, 8, dev)
+    assert b.data_ptr() == p0                      # same size: no allocation
+    c, _ = ws.get(3, 4, 1, 8, dev)                 # grows
+    assert ws.current(dev)[0].numel() >= 2 * 64
+    assert ws._retired[dev][0][0].data_ptr() == p0  # the old buffer is kept alive
+    d, _ = ws.get(4, 4, 1, 8, dev)                 # within the 2x growth: no new buffer
+    assert d.data_ptr() == c.data_ptr() and len(ws._retired[dev]) == 1

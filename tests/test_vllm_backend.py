@@ -10,6 +10,7 @@ import pytest
 import torch
 
 from integration import vllm_backend as vb
+from pagedattn import flat_splits_for, plan_decode, plan_launch
 
 
 class FakeBaseImpl:
@@ -92,7 +93,9 @@ def test_reason_to_delegate(impl_over, meta_over, kv, out, scale, expect):
 
 def test_forward_routes(monkeypatch):
     Backend, Impl = vb.build_backend_classes(FakeBaseBackend, FakeBaseImpl)
-    assert Backend.get_name() == vb.BACKEND_NAME and Backend.get_impl_cls() is Impl
+    assert Backend.get_impl_cls() is Impl
+    # the reference backend's registered name (vllm_backend.py:154-156)
+    assert Backend.get_name() == vb.BACKEND_NAME == "PAGEDATTN_TRITON"
     seen = []
     monkeypatch.setattr(vb, "decode_forward", lambda *a: seen.append(a) or "ours")
     q = torch.zeros(4, 32, 128, dtype=torch.float16)
@@ -135,7 +138,7 @@ def test_decode_forward_builds_the_cache_view(monkeypatch):
     assert cache.block_size == 16 and cache.kv_dtype == "fp16"
     assert cache.block_table.shape[0] == 2 and torch.equal(cache.seq_lens, meta.seq_lens[:2])
     assert (cache.shape.num_q_heads, cache.shape.num_kv_heads, cache.shape.head_dim) == (32, 8, 128)
-    assert c["num_splits"] == vb.pick_num_splits(2, 8, 300, 256)
+    assert c["num_splits"] == plan_launch(2, 300, 8, 4, 256).num_splits > 1
     assert c["sm_scale"] == impl.scale and c["max_seq_len"] == 300
     assert vb.STATS == {"decode_calls": 1, "decode_tokens": 2, "delegated_calls": 0}
     # a layer sharing another layer's KV does not write
@@ -201,18 +204,19 @@ def test_decode_forward_takes_the_flat_split_for_large_batches(monkeypatch):
                  seq_lens=torch.full((n,), 4096, dtype=torch.int32))
     impl.kv_sharing_target_layer_name = "shared"
     vb.decode_forward(impl, None, q, q, q, _kv(), meta, torch.zeros_like(q), decode=fake_decode)
-    assert calls[-1] == {"flat_splits": vb.flat_splits_for(8, 4, 256, 2)}
+    assert calls[-1] == {"flat_splits": flat_splits_for(8, 4, 256, 2)}
     # a small step stays on the classic split
     meta = _meta(max_seq_len=300)
     vb.decode_forward(impl, None, q, q, q, _kv(), meta, torch.zeros_like(q), decode=fake_decode)
-    assert calls[-1] == {"num_splits": vb.pick_num_splits(2, 8, 300, 256), "max_seq_len": 300}
+    assert calls[-1] == plan_launch(2, 300, 8, 4, 256).launch_kwargs() and "num_splits" in calls[-1]
     # so does a single long sequence (its classic merge is shorter than the flat one)
     meta = _meta(num_actual_tokens=1, max_seq_len=16384,
                  block_table=torch.zeros((1, 1024), dtype=torch.int32),
                  seq_lens=torch.full((1,), 16384, dtype=torch.int32))
     vb.decode_forward(impl, None, q[:1], q[:1], q[:1], _kv(), meta, torch.zeros_like(q[:1]),
                       decode=fake_decode)
-    assert calls[-1] == {"num_splits": vb.pick_num_splits(1, 8, 16384, 256), "max_seq_len": 16384}
+    assert calls[-1] == {"num_splits": plan_launch(1, 16384, 8, 4, 256).num_splits, "max_seq_len": 16384}
+    assert calls[-1]["num_splits"] > 1
 
 
 @pytest.mark.parametrize("dtype,limit", [(torch.float16, 1024), (torch.bfloat16, 1024)],
@@ -239,7 +243,7 @@ def test_decode_forward_runs_large_short_batches_unsplit(monkeypatch, dtype, lim
                      seq_lens=torch.full((n,), msl, dtype=torch.int32))
         vb.decode_forward(impl, None, q, q, q, _kv(dtype), meta, torch.zeros_like(q), decode=fake_decode)
         if want_flat:
-            assert calls[-1] == {"flat_splits": vb.flat_splits_for(8, 4, 256, 1)}
+            assert calls[-1] == {"flat_splits": flat_splits_for(8, 4, 256, 1)}
         else:
             assert calls[-1] == {"num_splits": 1, "max_seq_len": msl}
     # half the batch (4 workgroups per CU) keeps the flat split
@@ -248,4 +252,186 @@ def test_decode_forward_runs_large_short_batches_unsplit(monkeypatch, dtype, lim
                  seq_lens=torch.full((n // 2,), limit, dtype=torch.int32))
     vb.decode_forward(impl, None, q[: n // 2], q[: n // 2], q[: n // 2], _kv(dtype), meta,
                       torch.zeros_like(q[: n // 2]), decode=fake_decode)
-    assert calls[-1] == {"flat_splits": vb.flat_splits_for(8, 4, 256, 1)}
+    assert calls[-1] == {"flat_splits": flat_splits_for(8, 4, 256, 1)}
+
+
+def _boundary_plan(monkeypatch, lens, msl=None, host_lens=True, kv=torch.float16, shape=(32, 8, 128)):
+    """The launch keywords the boundary's decode_forward picks for a step."""
+    monkeypatch.setattr(vb, "_cu_count", lambda dev: 256)
+    monkeypatch.setattr(vb, "flat_waves_per_simd", lambda kv_dtype, d: 1)
+    calls = []
+
+    def fake_decode(q, cache, out, sm_scale, **kw):
+        calls.append(kw)
+
+    hq, hkv, d = shape
+    impl = FakeBaseImpl(num_heads=hq, num_kv_heads=hkv, head_size=d)
+    impl.kv_sharing_target_layer_name = "shared"
+    n = len(lens)
+    t = torch.tensor(lens, dtype=torch.int32)
+    extra = {"seq_lens_cpu": t} if host_lens else {}
+    meta = _meta(num_actual_tokens=n, max_seq_len=msl if msl is not None else max(lens),
+                 block_table=torch.zeros((n, 4), dtype=torch.int32), seq_lens=t, **extra)
+    q = torch.zeros(n, hq, d, dtype=kv)
+    kvc = torch.zeros((2, 4, 16, hkv, d), dtype=kv)
+    vb.decode_forward(impl, None, q, q, q, kvc, meta, torch.zeros_like(q), decode=fake_decode)
+    return calls[-1]
+
+
+def _wrapper_plan(lens, kv="fp16", shape=(32, 8, 128)):
+    """The launch `paged_decode_hip(num_splits=None)` plans for the same batch."""
+    hq, hkv, d = shape
+    s, m, f = plan_decode(lens, hkv, hq // hkv, 256, 1, kv_dtype=kv, head_dim=d)
+    return {"flat_splits": f} if f else {"num_splits": s, "max_seq_len": m}
+
+
+UNIFORM = [(b, t) for b in (1, 4, 24, 32, 64, 128, 256, 512, 1024, 1100)
+           for t in (16, 200, 256, 1024, 1056, 4096, 16384, 70000)]
+
+
+@pytest.mark.parametrize("shape", [(32, 8, 128), (64, 8, 128), (14, 2, 64)], ids=["8b", "70b", "qwen"])
+@pytest.mark.parametrize("kv", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+def test_boundary_plans_as_the_wrapper_with_host_lengths(monkeypatch, shape, kv):
+    """One planner: with the step's lengths on the host (`seq_lens_cpu`), the
+    boundary's launch is the one the decode wrapper plans, for uniform and
+    ragged batches."""
+    name = "bf16" if kv == torch.bfloat16 else "fp16"
+    g = torch.Generator().manual_seed(1)
+    batches = [[t] * b for b, t in UNIFORM if b * t <= 4_000_000]
+    batches += [torch.randint(1, hi, (b,), generator=g).tolist()
+                for b in (3, 64, 200, 512) for hi in (300, 3000, 40000) if b * hi <= 4_000_000]
+    for lens in batches:
+        assert _boundary_plan(monkeypatch, lens, kv=kv, shape=shape) == _wrapper_plan(lens, name, shape), \
+            (len(lens), max(lens))
+
+
+@pytest.mark.parametrize("shape", [(32, 8, 128), (64, 8, 128), (14, 2, 64)], ids=["8b", "70b", "qwen"])
+def test_boundary_without_host_lengths_on_uniform_batches(monkeypatch, shape):
+    """Metadata with device-only lengths: the boundary plans from the batch
+    size and the longest length, as for a ragged batch. On uniform batches it
+    then picks the wrapper's launch except where the wrapper uses what only
+    the lengths tell: a nearly uniform batch that fills the CUs unsplit runs
+    unsplit there (short sequences, or K/V under the per-CU byte limit),
+    while the boundary keeps the flat split, which ragged batches need."""
+    from pagedattn.hip_decode import _fills_unsplit
+
+    hq, hkv, d = shape
+    for b, t in UNIFORM:
+        if b * t > 4_000_000:
+            continue
+        lens = [t] * b
+        got = _boundary_plan(monkeypatch, lens, host_lens=False, shape=shape)
+        want = _wrapper_plan(lens, "fp16", shape)
+        if got != want:
+            assert want == {"num_splits": 1, "max_seq_len": t}, (b, t, got, want)
+            assert "flat_splits" in got and _fills_unsplit(lens, hkv, hq // hkv, 256), (b, t)
+        # the same plan as plan_launch from (batch, max_seq_len) alone
+        p = plan_launch(b, t, hkv, hq // hkv, 256, 1, kv_dtype="fp16", head_dim=d)
+        assert got == p.launch_kwargs()
+
+
+def test_host_seq_lens_reads_cpu_copies_only():
+    assert vb._host_seq_lens(types.SimpleNamespace(), 2) is None
+    assert vb._host_seq_lens(types.SimpleNamespace(seq_lens_cpu=None), 2) is None
+    m = types.SimpleNamespace(seq_lens_cpu=torch.tensor([5, 6, 7], dtype=torch.int32))
+    assert vb._host_seq_lens(m, 2) == [5, 6]
+
+
+class _NHDBackend:
+    @staticmethod
+    def get_kv_cache_shape(num_blocks, block_size, num_kv_heads, head_size):
+        return (2, num_blocks, block_size, num_kv_heads, head_size)
+
+
+class _FastImpl(FakeBaseImpl):
+    def forward(self, layer, query, key, value, kv_cache, attn_metadata, output=None,
+                output_scale=None):
+        self.base_calls += 1
+        return "fast-prefill"
+
+
+class _PagedLayoutBackend:
+    @staticmethod
+    def get_kv_cache_shape(num_blocks, block_size, num_kv_heads, head_size):
+        return (2, num_blocks, block_size * num_kv_heads * head_size)
+
+
+@pytest.fixture
+def fake_bases(monkeypatch):
+    """Stand-in vLLM backend modules: rocm_aiter_fa, triton_attn and an
+    `aiter` package, plus a base with the paged (non-NHD) layout."""
+    aiter_mod = types.ModuleType("vllm.v1.attention.backends.rocm_aiter_fa")
+    aiter_mod.AiterFlashAttentionBackend = type("AiterFlashAttentionBackend", (_NHDBackend,), {})
+    aiter_mod.AiterFlashAttentionImpl = type("AiterFlashAttentionImpl", (_FastImpl,), {})
+    triton_mod = types.ModuleType("vllm.v1.attention.backends.triton_attn")
+    triton_mod.TritonAttentionBackend = type("TritonAttentionBackend", (_NHDBackend,), {})
+    triton_mod.TritonAttentionImpl = type("TritonAttentionImpl", (FakeBaseImpl,), {})
+    other = types.ModuleType("stand_in_backends")
+    other.PagedBackend = _PagedLayoutBackend
+    other.PagedImpl = FakeBaseImpl
+    monkeypatch.setitem(__import__("sys").modules, aiter_mod.__name__, aiter_mod)
+    monkeypatch.setitem(__import__("sys").modules, triton_mod.__name__, triton_mod)
+    monkeypatch.setitem(__import__("sys").modules, other.__name__, other)
+    # use_base rebinds module globals: restore them after the test
+    for name in ("PagedAttnTritonBackend", "PagedAttnTritonImpl", "BASE_NAME"):
+        monkeypatch.setattr(vb, name, getattr(vb, name))
+    return aiter_mod, triton_mod
+
+
+def test_prefill_backend_choice_keeps_decode_on_the_kernel(monkeypatch, fake_bases):
+    aiter_mod, _ = fake_bases
+    assert vb.use_base("rocm_aiter_fa") == "rocm_aiter_fa" == vb.BASE_NAME
+    Backend, Impl = vb.PagedAttnTritonBackend, vb.PagedAttnTritonImpl
+    assert issubclass(Backend, aiter_mod.AiterFlashAttentionBackend)
+    assert issubclass(Impl, aiter_mod.AiterFlashAttentionImpl)
+    assert Backend.get_name() == "PAGEDATTN_TRITON" and Backend.get_impl_cls() is Impl
+    seen = []
+    monkeypatch.setattr(vb, "decode_forward", lambda *a: seen.append(a) or "ours")
+    q = torch.zeros(4, 32, 128, dtype=torch.float16)
+    impl = Impl()
+    # pure decode: the HIP kernel; prefill and mixed batches: the chosen base
+    assert impl.forward(None, q, q, q, _kv(), _meta(), torch.zeros_like(q)) == "ours"
+    assert impl.forward(None, q, q, q, _kv(), _meta(max_query_len=9), torch.zeros_like(q)) == "fast-prefill"
+    assert len(seen) == 1 and impl.base_calls == 1
+    # QUALNAME resolves to the rebuilt class
+    mod_name, cls_name = vb.QUALNAME.rsplit(".", 1)
+    assert getattr(__import__("importlib").import_module(mod_name), cls_name) is Backend
+
+
+def test_auto_base_prefers_aiter_when_it_imports(monkeypatch, fake_bases):
+    import sys
+
+    monkeypatch.setitem(sys.modules, "aiter", types.ModuleType("aiter"))
+    assert vb.resolve_base("auto")[0] == "rocm_aiter_fa"
+    monkeypatch.setitem(sys.modules, "aiter", None)  # import aiter raises ImportError
+    name, backend, impl = vb.resolve_base("auto")
+    assert name == "triton" and backend.__name__ == "TritonAttentionBackend"
+    assert vb.resolve_base(None)[0] == "triton"
+
+
+def test_base_with_another_cache_layout_is_refused(fake_bases):
+    with pytest.raises(ValueError, match="lays its KV cache out"):
+        vb.use_base("stand_in_backends:PagedBackend:PagedImpl")
+    with pytest.raises(ValueError, match="unknown base backend"):
+        vb.use_base("no_such_base")
+    with pytest.raises(ValueError, match="no get_kv_cache_shape"):
+        vb.check_nhd_layout(FakeBaseBackend)
+
+
+def test_install_with_a_prefill_backend(monkeypatch, fake_bases):
+    class Platform:
+        @classmethod
+        def get_attn_backend_cls(cls, *a):
+            return "x"
+
+    assert vb.install(Platform, prefill_backend="rocm_aiter_fa") == vb.QUALNAME
+    assert vb.BASE_NAME == "rocm_aiter_fa"
+    assert Platform.get_attn_backend_cls(None, 128, torch.float16, "auto", 16, True, False) == vb.QUALNAME
+
+    class Platform2(Platform):
+        pass
+
+    monkeypatch.setenv("PAGEDATTN_VLLM_BACKEND", "1")
+    monkeypatch.setenv("PAGEDATTN_PREFILL_BACKEND", "triton")
+    assert vb.maybe_install_from_env(Platform2) is True
+    assert vb.BASE_NAME == "triton"
