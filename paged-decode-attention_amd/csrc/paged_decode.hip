@@ -42,23 +42,21 @@
 // on most tiles. This is exact algebra (the normaliser uses the same stale
 // maximum); probabilities stay <= 2^kRescaleLog2, far from fp16 overflow.
 //
-// Quantised KV is dequantised in registers with one v_perm per fp16 pair:
+// Quantised KV is dequantised in registers to the fp16 values the reference's
+// dequantised cache holds (pagedattn/cache.py:51-62), with one v_perm per
+// fp16 pair:
 //   fp8_e5m2 -> fp16: the e5m2 byte is the high byte of the fp16 pattern.
-//   int8 K: no dequant. Q is held per head as 16-bit fixed point,
-//        round(q * 2^e) = 256 * hi + lo with hi, lo in int8, and two
-//        v_mfma_i32_16x16x64_i8 per 64 head dims give the integer score
-//        256 * (K.hi) + K.lo exactly; 2^-e times the per-(token, head) scale
-//        times qk_scale makes it the fp32 score. The fixed point moves each
-//        q element by at most 2^-14 of its head's max|q|.
-//   int8 V: with the byte's sign bit flipped (one xor per 4 bytes),
+//   int8 K and V: with the byte's sign bit flipped (one xor per 4 bytes),
 //        b ^ 0x80 = x + 128 is the mantissa of an fp16 denormal,
 //        (x + 128) * 2^-24, exact (v_fma_mix keeps fp16 denormals); one
 //        v_fma_mix per element forms fp16((x + 128) * 2^-24 * s * 2^24
 //        - 128 * s) = fp16(x * s), the product rounded once to fp32 and then
-//        to fp16 as the reference's dequantised cache holds it, and P goes to
-//        the MFMA in fp16 as for an fp16 cache. (Folding s into P instead
-//        would round s to fp16: a one-token sequence then returns
-//        x * fp16(s), up to 2^-11 relative away from fp16(x * s).)
+//        to fp16 as the reference's kernel rounds it
+//        (triton_decode.py:145-149). K then enters the fp16 QK MFMA and V
+//        the fp16 PV MFMA exactly as an fp16 cache's rows would. (Skipping
+//        the fp16 rounding of K, i.e. attending over the exact x * s, moves
+//        the output by up to ~2e-3 from the reference's on peaked heads;
+//        folding s into P instead would round s to fp16.)
 
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
@@ -78,7 +76,6 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 4;          // waves per workgroup (unsplit / classic split)
 constexpr int kFlatWaves = 4;      // flat kernel: one wave per SIMD of a CU
@@ -162,21 +159,6 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
   return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
-// Per-half unsigned 16-bit maximum of two packed pairs.
-__device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
-  typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
-  const u16x2 x = __builtin_bit_cast(u16x2, a), y = __builtin_bit_cast(u16x2, b);
-  return __builtin_bit_cast(uint32_t, u16x2{x[0] > y[0] ? x[0] : y[0], x[1] > y[1] ? x[1] : y[1]});
-}
-
-// floor(x) as int32 in one instruction (the compiler keeps floor and the
-// conversion apart).
-__device__ __forceinline__ int cvt_flr_i32(float x) {
-  int r;
-  asm("v_cvt_flr_i32_f32 %0, %1" : "=v"(r) : "v"(x));
-  return r;
-}
-
 __device__ __forceinline__ f16x8 as_f16x8(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
   u32x4 u = {w0, w1, w2, w3};
   return __builtin_bit_cast(f16x8, u);
@@ -231,6 +213,46 @@ __device__ __forceinline__ constexpr uint32_t pair_sel(uint32_t i, uint32_t j) {
 template <int KV>
 __device__ __forceinline__ uint32_t bytes_to_halves(uint32_t hi, uint32_t lo, uint32_t sel) {
   return perm(hi, lo, sel);
+}
+
+// Two fp32 values -> an fp16 pair, each rounded to nearest even
+// (v_cvt_pk_f16_f32). The empty asm statements hide where a and b come from,
+// so the compiler converts the fp32 values as they are instead of folding
+// the conversion into the fma that produced them (v_fma_mixlo/hi_f16, which
+// runs at a third of the rate of ordinary VALU ops when waves share a SIMD).
+// They emit no instruction: an instruction written in asm escapes the
+// compiler's hazard checks, and an MFMA reading its result one instruction
+// later read a stale register.
+__device__ __forceinline__ uint32_t cvt_pk_f16(float a, float b) {
+  asm("" : "+v"(a));
+  asm("" : "+v"(b));
+  const f16x2 h = {(_Float16)a, (_Float16)b};
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+// int8 -> fp16(x * s), the reference's dequantised value (cache.py:51-62;
+// triton_decode.py:145-149: the fp32 product rounded to fp16), for a pair of
+// stored bytes whose sign bits are already flipped (b ^ 0x80 = x + 128).
+//   fp16 scales: the byte under the exponent byte 0x64 is the fp16 value
+//     1024 + (x + 128); minus 1152 it is x, exactly, and one fp16 multiply
+//     by s rounds the exact product x * s once (an 8-bit x times an 11-bit s
+//     is exact in fp32, so this equals the reference's two roundings).
+//     `lo` holds both bytes (positions i, j); 3 packed ops per pair.
+//   fp32 scales: the byte as the fp16 denormal (x + 128) * 2^-24 (exact), one
+//     fma per element in fp32 with s * 2^24 and -128 * s gives fp32(x * s),
+//     then a round to fp16: the reference's fp32 product and fp16 cast.
+constexpr uint32_t kF16Exp1024 = 0x64646464u;  // exponent byte of 1024 in every byte
+
+__device__ __forceinline__ uint32_t i8pair_fp16_scale(uint32_t lo, uint32_t i, uint32_t j, uint32_t s2) {
+  const uint32_t h = perm(kF16Exp1024, lo, i | (4u << 8) | (j << 16) | (4u << 24));
+  const f16x2 x = __builtin_bit_cast(f16x2, h) - f16x2{(_Float16)1152.0f, (_Float16)1152.0f};
+  return __builtin_bit_cast(uint32_t, x * __builtin_bit_cast(f16x2, s2));
+}
+
+__device__ __forceinline__ uint32_t i8pair_fp32_scale(uint32_t den, float s0_24, float c0, float s1_24,
+                                                      float c1) {
+  const f16x2 u2 = __builtin_bit_cast(f16x2, den);
+  return cvt_pk_f16(__builtin_fmaf((float)u2[0], s0_24, c0), __builtin_fmaf((float)u2[1], s1_24, c1));
 }
 
 // A raw buffer over the `bytes` bytes from `base` on: a load at a per-lane
@@ -294,7 +316,6 @@ template <int KV, int D>
 struct Geo {
   static constexpr int kElem = (KV == PA_KV_FP16 || KV == PA_KV_BF16) ? 2 : 1;  // stored bytes/elem
   static constexpr int kKSteps = D / 32;                    // QK MFMAs per sub-tile (fp16 operands)
-  static constexpr int kQBlocks = (D + 63) / 64;            // int8: 64-wide QK blocks
   static constexpr int kE = D / 16;                         // V elems per lane row
   static constexpr int kVBytes = kE * kElem;                // V bytes per lane row
   static constexpr int kVWords = (kVBytes + 3) / 4;
@@ -365,12 +386,6 @@ struct WaveState {
   f32x4 acc[G::kE];       // O^T accumulators, one 16x16 block per d-slab
   float m;                // running max (log2 domain) for head column r16
   float l;                // running sum over this lane's tokens
-  // int8 only: head r16's q as 16-bit fixed point, round(q * 2^e) = 256 * hi
-  // + lo with hi, lo in int8, as i8 MFMA B-operands (lane c holds head dims
-  // 64 * blk + 16c .. +15), and qinv = 2^-e
-  i32x4 qhi[G::kQBlocks];
-  i32x4 qlo[G::kQBlocks];
-  float qinv;
 };
 
 // Issue the loads of the tile starting at token n0 (< hi). A tile is two
@@ -468,14 +483,15 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
   // ---- int8 scales of this tile into the wave's LDS slot; each lane reads
-  // back those of its tokens {16u + 4c + i} where they are used (K after the
-  // QK products, V for the P operand), so none are live across the MFMAs ----
+  // back those of the rows it dequantises (K: its operand row r16 of each
+  // sub-tile; V: its tokens {16u + 4c + i} for the P operand), so none are
+  // live across the loads ----
   if constexpr (KV == PA_KV_INT8) {
-    // (entries 0 .. kTT-1 are K scales, stored times qk_scale, the rest V
-    // scales, stored times 2^24)
+    // (entries 0 .. kTT-1 are K scales, the rest V scales; fp32 scales
+    // stored times 2^24, fp16 scales as they are)
 #pragma unroll
     for (int j = 0; j < G::kScales / 64; ++j)
-      sc_lds[j * 64 + lane] = r.sc[j] * ((j * 64 + lane >= G::kTT) ? kInt8Unit : p.qk_scale);
+      sc_lds[j * 64 + lane] = SC == PA_SCALE_FP32 ? r.sc[j] * kInt8Unit : r.sc[j];
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -486,38 +502,49 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
 #pragma unroll
   for (int u = 0; u < NS; ++u) {
     f32x4 a = {0.f, 0.f, 0.f, 0.f};
+    // int8: every element of this lane's operand is in row r16 of the
+    // sub-tile, so one scale serves them all (fp32 scales: ks8 = s * 2^24,
+    // kc8 = -128 * s; fp16 scales: the pair ks2 = (s, s))
+    float ks8 = 0.f, kc8 = 0.f;
+    uint32_t ks2 = 0;
     if constexpr (KV == PA_KV_INT8) {
-      // int8 K bytes straight from LDS against Q's two int8 halves: the
-      // integer score 256 * (K.hi) + K.lo is exact in int32
-      i32x4 ahi = {0, 0, 0, 0}, alo = {0, 0, 0, 0};
+      ks8 = sc_lds[16 * u + r16];
+      kc8 = ks8 * (-1.0f / 131072.0f);
+      if constexpr (SC == PA_SCALE_FP16) ks2 = cvt_pk_f16(ks8, ks8);
+    }
 #pragma unroll
-      for (int kb = 0; kb < G::kQBlocks; ++kb) {
-        // head_dim 32: lanes c >= 2 have zero Q and read a valid row piece
-        const int col = D >= 64 ? 64 * kb + 16 * c : 16 * (c & 1);
-        const i32x4 kop = *reinterpret_cast<const i32x4 *>(k_lds + (16 * u + r16) * G::kKSlotStride + col);
-        ahi = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop, st.qhi[kb], ahi, 0, 0, 0);
-        alo = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop, st.qlo[kb], alo, 0, 0, 0);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = (float)((ahi[i] << 8) + alo[i]);
-    } else {
-#pragma unroll
-      for (int ks = 0; ks < G::kKSteps; ++ks) {
-        f16x8 kop;
-        const uint8_t *src = k_lds + (16 * u + r16) * G::kKSlotStride + (32 * ks + 8 * c) * G::kElem;
-        if constexpr (KV == PA_KV_BF16) {
-          kop = bf16x8_to_f16x8(*reinterpret_cast<const u32x4 *>(src));
-        } else if constexpr (G::kElem == 2) {
-          kop = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4 *>(src));
+    for (int ks = 0; ks < G::kKSteps; ++ks) {
+      f16x8 kop;
+      const uint8_t *src = k_lds + (16 * u + r16) * G::kKSlotStride + (32 * ks + 8 * c) * G::kElem;
+      if constexpr (KV == PA_KV_BF16) {
+        kop = bf16x8_to_f16x8(*reinterpret_cast<const u32x4 *>(src));
+      } else if constexpr (G::kElem == 2) {
+        kop = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4 *>(src));
+      } else if constexpr (KV == PA_KV_INT8) {
+        // the reference's dequantised K, fp16(x * s) per element
+        const u32x2 w = *reinterpret_cast<const u32x2 *>(src);
+        const uint32_t w0 = w.x ^ kInt8Sign, w1 = w.y ^ kInt8Sign;
+        uint32_t dq[4];
+        if constexpr (SC == PA_SCALE_FP16) {
+          dq[0] = i8pair_fp16_scale(w0, 0, 1, ks2);
+          dq[1] = i8pair_fp16_scale(w0, 2, 3, ks2);
+          dq[2] = i8pair_fp16_scale(w1, 0, 1, ks2);
+          dq[3] = i8pair_fp16_scale(w1, 2, 3, ks2);
         } else {
-          const u32x2 w = *reinterpret_cast<const u32x2 *>(src);
-          kop = as_f16x8(bytes_to_halves<KV>(w.x, w.x, pair_sel<KV>(0, 1)),
-                         bytes_to_halves<KV>(w.x, w.x, pair_sel<KV>(2, 3)),
-                         bytes_to_halves<KV>(w.y, w.y, pair_sel<KV>(0, 1)),
-                         bytes_to_halves<KV>(w.y, w.y, pair_sel<KV>(2, 3)));
+          dq[0] = i8pair_fp32_scale(perm(w0, w0, pair_sel<KV>(0, 1)), ks8, kc8, ks8, kc8);
+          dq[1] = i8pair_fp32_scale(perm(w0, w0, pair_sel<KV>(2, 3)), ks8, kc8, ks8, kc8);
+          dq[2] = i8pair_fp32_scale(perm(w1, w1, pair_sel<KV>(0, 1)), ks8, kc8, ks8, kc8);
+          dq[3] = i8pair_fp32_scale(perm(w1, w1, pair_sel<KV>(2, 3)), ks8, kc8, ks8, kc8);
         }
-        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, st.qop[ks], a, 0, 0, 0);
+        kop = as_f16x8(dq[0], dq[1], dq[2], dq[3]);
+      } else {
+        const u32x2 w = *reinterpret_cast<const u32x2 *>(src);
+        kop = as_f16x8(bytes_to_halves<KV>(w.x, w.x, pair_sel<KV>(0, 1)),
+                       bytes_to_halves<KV>(w.x, w.x, pair_sel<KV>(2, 3)),
+                       bytes_to_halves<KV>(w.y, w.y, pair_sel<KV>(0, 1)),
+                       bytes_to_halves<KV>(w.y, w.y, pair_sel<KV>(2, 3)));
       }
+      a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, st.qop[ks], a, 0, 0, 0);
     }
     sacc[u] = a;
   }
@@ -527,17 +554,8 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
 
   // ---- online softmax over the tokens this lane holds for head r16 ----
   float s[NV];
-  if constexpr (KV == PA_KV_INT8) {
 #pragma unroll
-    for (int u = 0; u < NS; ++u) {
-      const f32x4 kq = *reinterpret_cast<const f32x4 *>(sc_lds + 16 * u + 4 * c);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) s[4 * u + i] = sacc[u][i] * (kq[i] * st.qinv);
-    }
-  } else {
-#pragma unroll
-    for (int e = 0; e < NV; ++e) s[e] = sacc[e >> 2][e & 3] * p.qk_scale;
-  }
+  for (int e = 0; e < NV; ++e) s[e] = sacc[e >> 2][e & 3] * p.qk_scale;
   if (tail) {
 #pragma unroll
     for (int e = 0; e < NV; ++e) {
@@ -590,8 +608,11 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
       }
     } else {
       // int8: element e of the lane's operand is token 16 * (2pp + e / 4)
-      // + 4c + e % 4, with V scale vs[e] = s * 2^24 and vc[e] = -128 * s
+      // + 4c + e % 4, with V scale vs[e] (fp32 scales: s * 2^24, and
+      // vc[e] = -128 * s; fp16 scales: s, and the pairs vs2[m2] = (vs[2m2],
+      // vs[2m2 + 1]))
       float vs[8], vc[8];
+      uint32_t vs2[4];
       if constexpr (KV == PA_KV_INT8) {
 #pragma unroll
         for (int h2 = 0; h2 < 2; ++h2) {
@@ -601,6 +622,10 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
             vs[4 * h2 + i] = vq[i];
             vc[4 * h2 + i] = vq[i] * (-1.0f / 131072.0f);
           }
+        }
+        if constexpr (SC == PA_SCALE_FP16) {
+#pragma unroll
+          for (int m2 = 0; m2 < 4; ++m2) vs2[m2] = cvt_pk_f16(vs[2 * m2], vs[2 * m2 + 1]);
         }
       }
       // word wi of a row holds head-dim elements 4*wi .. 4*wi+3 of the lane's
@@ -619,11 +644,14 @@ __device__ __forceinline__ void compute_tile(WaveState<KV, D> &st, const Tile<KV
 #pragma unroll
         for (int m2 = 0; m2 < 4; ++m2) {
           h[m2] = bytes_to_halves<KV>(vw[2 * m2 + 1][wi], vw[2 * m2][wi], pair_sel<KV>(b, b));
-          if constexpr (KV == PA_KV_INT8) {
-            const f16x2 u2 = __builtin_bit_cast(f16x2, h[m2]);
-            const f16x2 x2 = {(_Float16)__builtin_fmaf((float)u2[0], vs[2 * m2], vc[2 * m2]),
-                              (_Float16)__builtin_fmaf((float)u2[1], vs[2 * m2 + 1], vc[2 * m2 + 1])};
-            h[m2] = __builtin_bit_cast(uint32_t, x2);
+          if constexpr (KV == PA_KV_INT8 && SC == PA_SCALE_FP16) {
+            // the two bytes come from two rows: zero-extended halves x + 128,
+            // under the exponent byte 0x64 (see i8pair_fp16_scale)
+            const f16x2 x2 = __builtin_bit_cast(f16x2, h[m2] | 0x64006400u) -
+                             f16x2{(_Float16)1152.0f, (_Float16)1152.0f};
+            h[m2] = __builtin_bit_cast(uint32_t, x2 * __builtin_bit_cast(f16x2, vs2[m2]));
+          } else if constexpr (KV == PA_KV_INT8) {
+            h[m2] = i8pair_fp32_scale(h[m2], vs[2 * m2], vc[2 * m2], vs[2 * m2 + 1], vc[2 * m2 + 1]);
           }
         }
         const f16x8 vop = as_f16x8(h[0], h[1], h[2], h[3]);
@@ -657,54 +685,8 @@ __device__ __forceinline__ void load_q(WaveState<KV, D> &st, const KParams &p, i
     }
     return qv;
   };
-  if constexpr (KV != PA_KV_INT8) {
 #pragma unroll
-    for (int ks = 0; ks < G::kKSteps; ++ks) st.qop[ks] = q8(32 * ks + 8 * c);
-  } else {
-    // lane c holds head dims 64 * blk + 16c .. +15 (head_dim 32: lanes c < 2).
-    // max|q| on the fp16 bit patterns: with the sign cleared they order as
-    // the values do, two per v_pk_max_u16
-    constexpr int NB = G::kQBlocks;
-    f16x8 qh[NB][2];
-    uint32_t mx = 0;
-#pragma unroll
-    for (int kb = 0; kb < NB; ++kb) {
-      const int d0 = 64 * kb + 16 * c;
-      const bool live = D >= 64 || c < 2;
-#pragma unroll
-      for (int hlf = 0; hlf < 2; ++hlf) {
-        qh[kb][hlf] = live ? q8(d0 + 8 * hlf) : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-        const u32x4 w = __builtin_bit_cast(u32x4, qh[kb][hlf]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) mx = pk_max_u16(mx, w[i] & 0x7fff7fffu);
-      }
-    }
-    float amax = (float)__builtin_bit_cast(_Float16, (uint16_t)max(mx & 0xffffu, mx >> 16));
-    amax = col_max(amax);
-    // amax in [2^(x-1), 2^x): scaled by 2^(14 - x) it is below 2^14, so
-    // |Q| = |round(q * 2^e)| <= 2^14 and hi = (Q + 128) >> 8 stays within
-    // +-64, lo = Q - 256 hi within -128 .. 127. With t = Q + 128 (one fma
-    // and a floor: round half up), hi is byte 1 of t and lo byte 0 of t
-    // with its top bit flipped.
-    const int e = amax > 0.f ? 14 - __builtin_amdgcn_frexp_expf(amax) : 0;
-    st.qinv = __builtin_ldexpf(1.0f, -e);
-    const float sc = __builtin_ldexpf(1.0f, e);
-#pragma unroll
-    for (int kb = 0; kb < NB; ++kb) {
-      uint32_t hw[4], lw[4];
-#pragma unroll
-      for (int w4 = 0; w4 < 4; ++w4) {
-        uint32_t t[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          t[j] = (uint32_t)cvt_flr_i32(__builtin_fmaf((float)qh[kb][w4 >> 1][4 * (w4 & 1) + j], sc, 128.5f));
-        hw[w4] = perm(t[1], t[0], 0x0c0c0501u) | perm(t[3], t[2], 0x05010c0cu);
-        lw[w4] = (perm(t[1], t[0], 0x0c0c0400u) | perm(t[3], t[2], 0x04000c0cu)) ^ kInt8Sign;
-      }
-      st.qhi[kb] = i32x4{(int)hw[0], (int)hw[1], (int)hw[2], (int)hw[3]};
-      st.qlo[kb] = i32x4{(int)lw[0], (int)lw[1], (int)lw[2], (int)lw[3]};
-    }
-  }
+  for (int ks = 0; ks < G::kKSteps; ++ks) st.qop[ks] = q8(32 * ks + 8 * c);
 }
 
 template <int KV, int D>

@@ -109,7 +109,7 @@ def run(args, keep_state: bool = False):
     wps = flat_waves_per_simd(args.kv, shape.head_dim, sdt if args.kv == "int8" else None)
     # one launch for the whole run, planned as the vLLM boundary plans a step
     # (batch size and the longest length the run reaches, no host lengths)
-    flat = flat_splits_for(shape.num_kv_heads, shape.gqa_group, _cu_count(dev), wps)
+    flat = flat_splits_for(shape.num_kv_heads, shape.gqa_group, _cu_count(dev), wps, args.kv)
     mode = getattr(args, "launch", "plan")
     if mode == "flat":
         launch = {"flat_splits": flat}

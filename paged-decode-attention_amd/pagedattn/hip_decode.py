@@ -62,6 +62,13 @@ RAGGED_SPLIT_MIN_TILES = 32
 # slower still). Used when each wave gets at least MIN_FLAT_TILES_PER_WAVE
 # 32-token tiles; smaller batches are latency-bound and run faster unsplit.
 FLAT_WAVES_PER_SIMD = 1
+# int8 tiles carry a dequantisation per K and V element (the reference's
+# fp16(x * s)), which keeps one wave per SIMD busy issuing VALU work: a
+# second wave per SIMD hides it. Decode kernel alone, one against two flat
+# waves per SIMD: Llama-3-70B shape B = 32, T = 16384 (C4) fp32 scales 192.4
+# / 176.3 us, fp16 scales 189.6 / 178.9; Llama-3-8B B = 64, T = 4096 fp32
+# 107.1 / 95.0, fp16 97.1 / 92.4; Qwen2.5 B = 256, T = 2048 41.7 / 38.0.
+FLAT_WAVES_PER_SIMD_KV = {"int8": 2}
 MIN_FLAT_TILES_PER_WAVE = 4
 # A single sequence up to this many tiles takes the classic split: cut into
 # one chunk per CU it merges 32 partials per head, the flat split 128 (graph-
@@ -234,11 +241,14 @@ def plan_num_splits(seq_lens, num_kv_heads: int, group: int, sm_count: int) -> t
     return int(splits), tmax
 
 
-def flat_splits_for(num_kv_heads: int, group: int, sm_count: int, waves_per_simd: int) -> int:
+def flat_splits_for(num_kv_heads: int, group: int, sm_count: int, waves_per_simd: int,
+                    kv_dtype: str | None = None) -> int:
     """One round of waves over the (kv head, head tile) units: as many as
     the CUs hold (4 SIMDs each, `waves_per_simd` waves per SIMD), capped at
-    FLAT_WAVES_PER_SIMD per SIMD."""
-    per_simd = max(1, min(waves_per_simd, FLAT_WAVES_PER_SIMD))
+    FLAT_WAVES_PER_SIMD per SIMD (FLAT_WAVES_PER_SIMD_KV for the KV types
+    that differ)."""
+    cap = FLAT_WAVES_PER_SIMD_KV.get(kv_dtype, FLAT_WAVES_PER_SIMD)
+    per_simd = max(1, min(waves_per_simd, cap))
     waves = max(1, sm_count) * SIMDS_PER_CU * per_simd
     return int(max(1, min(waves // _units(num_kv_heads, group), _abi.PA_MAX_FLAT_SPLITS)))
 
@@ -300,7 +310,7 @@ def plan_launch(batch: int, max_seq_len: int, num_kv_heads: int, group: int, sm_
     else:
         tmax = max(0, int(max_seq_len))
         tiles = batch * _tiles(tmax)  # an upper bound
-    flat = flat_splits_for(num_kv_heads, group, cus, waves_per_simd)
+    flat = flat_splits_for(num_kv_heads, group, cus, waves_per_simd, kv_dtype)
     flat_ok = (batch <= FLAT_MAX_BATCH and tiles >= MIN_FLAT_TILES_PER_WAVE * flat
                and not (batch == 1 and _tiles(tmax) <= SINGLE_SEQ_SPLIT_MAX_TILES))
     if flat_ok:

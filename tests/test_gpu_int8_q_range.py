@@ -1,19 +1,16 @@
-"""int8 caches: the QK product holds q per head in fixed point.
+"""int8 caches with query heads of very different magnitudes.
 
-For an int8 cache the kernel multiplies the stored K bytes with Q in two int8
-MFMAs. Q is first scaled per head by a power of two that puts max|q| in
-[2^13, 2^14) and rounded to an integer (15 bits and a sign). These tests give the heads of one kv group q
-magnitudes far apart: a zero head, 1e-3, 0.03, 1, 3 and a head with one
-dominant element. Each head then gets its own exponent, checked against the
-fp32 oracle (pagedattn/reference.py:28-49 restated) on every launch shape.
-
-The bound is the decode's 2e-3 plus 2^-10 |oracle|. The larger q heads
-concentrate the softmax, so outputs approach max|V| (about 4 here). There the
-fp16 probabilities, which the reference also uses (triton_decode.py:165), and
-the fp16 output each cost up to 2^-11 |out| whatever the q arithmetic. A CPU
-emulation of these inputs with exact q gives the same worst errors as the
-15-bit fixed point (1.5e-3 at D = 256). A zero head must return the plain
-mean of V (softmax of equal logits) within 2e-3.
+The heads of one kv group get q magnitudes far apart: a zero head, 1e-3, 0.03,
+1, 3 and a head with one dominant element. The large heads concentrate the
+softmax, which makes the output sensitive to how K is dequantised: the
+reference rounds every dequantised K element to fp16, fp16(x * s)
+(pagedattn/cache.py:51-62, triton_decode.py:145-149), and so does the kernel,
+so it meets the decode's plain 2e-3 bar against the fp32 oracle on the same
+dequantised cache (pagedattn/reference.py:28-49 restated) on every launch
+shape. tests/test_int8_reference_rounding.py shows on the CPU, on these same
+inputs, that the reference's rounding chain stays within 2e-3 while attending
+over the unrounded x * s would not. A zero head must return the plain mean of
+V (softmax of equal logits) within 2e-3.
 """
 
 from __future__ import annotations
@@ -56,10 +53,9 @@ def test_int8_heads_with_distant_q_magnitudes(sdt, d, launch):
     got = paged_decode_hip(q, c, **LAUNCHES[launch])
     torch.cuda.synchronize()
     want = oracle.reference_decode(q.cpu(), c, out_dtype=torch.float32)
-    err = (got.float().cpu() - want).abs()
-    excess = (err - (ABS_TOL + 2.0 ** -10 * want.abs())).max().item()
-    print(f"  max_abs={err.max().item():.2e} excess over the bound={excess:.2e}", flush=True)
-    assert excess < 0
+    err = (got.float().cpu() - want).abs().max().item()
+    print(f"  max_abs={err:.2e}", flush=True)
+    assert err < ABS_TOL
     # zero-q heads: equal logits, so the output is the mean of the dequantised V rows
     _, v = oracle.gather_contiguous(c)  # [B, Hkv, S, D] fp16
     for b, t in enumerate(LENS):

@@ -361,6 +361,11 @@ def test_flat_splits_for_and_plan_decode():
     assert flat_splits_for(8, 4, 256, 1) == 128
     assert flat_splits_for(2, 20, 256, 2) == 256      # group 20: two head tiles
     assert flat_splits_for(64, 1, 4, 1) == 1
+    # int8 caches take two waves per SIMD where the kernel's occupancy allows
+    assert flat_splits_for(8, 8, 256, 2, "int8") == 256
+    assert flat_splits_for(8, 8, 256, 1, "int8") == 128
+    assert flat_splits_for(8, 8, 256, 4, "fp8_e5m2") == 128
+    assert plan_decode([16384] * 32, 8, 8, 256, 2, kv_dtype="int8", head_dim=128) == (1, 16384, 256)
     # every benchmark config with a split (C2-C5) takes the flat split ...
     assert plan_decode([4096] * 64, 8, 4, 256, 2) == (1, 4096, 128)
     assert plan_decode([16384] * 32, 8, 8, 256, 3) == (1, 16384, 128)
