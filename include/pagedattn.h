@@ -24,7 +24,9 @@
  * a machine without a GPU. Launches are asynchronous on the stream passed in
  * (a hipStream_t, passed as void*; NULL means the legacy default stream).
  * The library allocates no device memory: the caller owns every buffer,
- * including the split-KV workspace (part_out / part_lse).
+ * including the split-KV workspace (part_out / part_lse), except that
+ * pa_decode_noalloc keeps its partials in a static device array that loads
+ * with the library's code object.
  *
  * Tensor layouts (element strides; the innermost dimension is contiguous):
  *   q          [batch, num_q_heads, head_dim]                  fp16 | bf16
@@ -55,7 +57,7 @@
 extern "C" {
 #endif
 
-#define PA_ABI_VERSION 4
+#define PA_ABI_VERSION 5
 
 /* Return codes. */
 #define PA_OK 0
@@ -239,6 +241,26 @@ int pa_flat_merge(const pa_decode_args *args, void *stream);
  * (its split count comes from the SM count alone,
  * pagedattn/triton_decode.py:248-263). */
 int pa_flat_waves_per_simd(int kv_dtype, int scale_dtype, int head_dim, int *out);
+
+/* Bytes of the static device scratch behind pa_decode_noalloc (per GPU). */
+#define PA_NOALLOC_SCRATCH_BYTES (32 << 20)
+
+/* pa_decode without a caller workspace, allocating nothing: no hipMalloc,
+ * no allocator call, for callers that cannot allocate (code under HIP graph
+ * capture, serving loops or harnesses that forbid allocation). The split
+ * partials go to a static device array of PA_NOALLOC_SCRATCH_BYTES inside
+ * the library, one per GPU, held until the process ends; its address is
+ * looked up once per device (hipGetSymbolAddress) on the first call there.
+ * part_out, part_lse and their strides in *args are ignored; everything
+ * else means what it means for pa_decode, and the results are pa_decode's.
+ * A launch whose partials need more than PA_NOALLOC_SCRATCH_BYTES
+ * (split: batch * num_splits, flat: batch + flat_splits slots of
+ * num_q_heads * (head_dim + 1) floats) returns PA_ERR_UNSUPPORTED. Every
+ * call on one GPU shares that GPU's array, so calls that overlap on one GPU
+ * (two streams, two threads) race: the caller serialises them. No
+ * counterpart in the reference, whose host wrapper allocates its workspace
+ * (pagedattn/triton_decode.py:266-282). */
+int pa_decode_noalloc(const pa_decode_args *args, void *stream);
 
 /* Message for the last non-zero return on the calling thread ("" if none). */
 const char *pa_last_error(void);

@@ -64,6 +64,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "pagedattn.h"
@@ -1732,6 +1733,40 @@ namespace {
 thread_local char g_err[512] = "";
 }  // namespace
 
+// The split partials of pa_decode_noalloc: one array per GPU, loaded with
+// the code object and held until the process ends. In host code `scratch`
+// only names the symbol for the runtime; kernels get the device address
+// that scratch_address() looks up.
+static __device__ __align__(256) uint8_t scratch[PA_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// This GPU's `scratch` address: hipGetSymbolAddress once per device, with
+// the device current, then the kept pointer.
+int scratch_address(void **out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return pa_fail(PA_ERR_HIP, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return pa_fail(PA_ERR_UNSUPPORTED, "device %d is beyond the %d the library keeps scratch for", dev,
+                   kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return pa_fail(PA_ERR_HIP, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                     hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return PA_OK;
+}
+}  // namespace
+
 int pa_fail(int code, const char *fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
@@ -1781,6 +1816,48 @@ int pa_decode(const pa_decode_args *a, void *stream) {
     if (e != hipSuccess) return fail(PA_ERR_HIP, "reduce launch failed: %s", hipGetErrorString(e));
   }
   return ok();
+}
+
+int pa_decode_noalloc(const pa_decode_args *a, void *stream) {
+  if (a == nullptr) return fail(PA_ERR_INVALID, "args is NULL");
+  pa_decode_args b = *a;
+  const bool flat = b.flat_splits > 0;
+  const bool split = flat || b.num_splits > 1;
+  b.part_out = nullptr;
+  b.part_lse = nullptr;
+  if (!split) return pa_decode(&b, stream);  // unsplit: no partials, no scratch
+  // every argument is validated (with a stand-in workspace address that is
+  // never used) before the size check and the first HIP call
+  float *const stand_in = reinterpret_cast<float *>(uintptr_t(256));
+  b.part_out = stand_in;
+  b.part_lse = stand_in;
+  b.stride_pb = b.stride_ph = b.stride_ps = b.stride_lb = b.stride_lh = 0;
+  KParams k;
+  int rc = build_params(&b, true, &k);
+  if (rc != PA_OK) return rc;
+  // packed partials: flat slots [batch + F, Hq, D] / [batch + F, Hq], or the
+  // classic [B, Hq, S, D] / [B, Hq, S] (sizes validated above)
+  const int64_t hq = b.num_q_heads, d = b.head_dim, s = flat ? 1 : b.num_splits;
+  b.stride_ph = s * d;
+  b.stride_pb = hq * s * d;
+  b.stride_ps = flat ? 0 : d;
+  b.stride_lh = s;
+  b.stride_lb = hq * s;
+  const int64_t slots = flat ? (int64_t)b.batch + b.flat_splits : (int64_t)b.batch * b.num_splits;
+  const int64_t rows = slots * hq;  // < 2^63: slots < 2^33, hq < 2^31
+  const int64_t cap = PA_NOALLOC_SCRATCH_BYTES;
+  const int64_t lse_off = rows <= cap ? (rows * d * 4 + 255) / 256 * 256 : cap + 1;
+  if (rows > cap / (4 * (d + 1)) || lse_off + rows * 4 > cap)
+    return fail(PA_ERR_UNSUPPORTED,
+                "%s needs %lld partial rows of %lld floats (plus their log-sum-exps), more than the "
+                "%lld-byte static scratch of pa_decode_noalloc holds",
+                flat ? "this flat split" : "this split", (long long)rows, (long long)d, (long long)cap);
+  void *base = nullptr;
+  rc = scratch_address(&base);
+  if (rc != PA_OK) return rc;
+  b.part_out = static_cast<float *>(base);
+  b.part_lse = reinterpret_cast<float *>(static_cast<uint8_t *>(base) + lse_off);
+  return pa_decode(&b, stream);
 }
 
 int pa_decode_partials(const pa_decode_args *a, void *stream) {

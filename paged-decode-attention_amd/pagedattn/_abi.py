@@ -12,7 +12,7 @@ import os
 import pathlib
 import threading
 
-PA_ABI_VERSION = 4
+PA_ABI_VERSION = 5
 
 PA_OK = 0
 PA_ERR_INVALID = -1
@@ -33,6 +33,7 @@ PA_IO_BF16 = 1
 
 PA_MAX_SPLITS = 4096
 PA_MAX_FLAT_SPLITS = 65536
+PA_NOALLOC_SCRATCH_BYTES = 32 << 20
 PA_MAX_GROUP = 16
 
 LIB_NAME = "libpagedattn_hip.so"
@@ -40,6 +41,7 @@ LIB_NAME = "libpagedattn_hip.so"
 # Every symbol include/pagedattn.h declares.
 EXPORTED_SYMBOLS = (
     "pa_decode",
+    "pa_decode_noalloc",
     "pa_decode_partials",
     "pa_split_reduce",
     "pa_cache_write",
@@ -178,6 +180,8 @@ def load() -> ctypes.CDLL:
         lib = ctypes.CDLL(str(path))
         lib.pa_decode.argtypes = [ctypes.POINTER(PaDecodeArgs), _vp]
         lib.pa_decode.restype = ctypes.c_int
+        lib.pa_decode_noalloc.argtypes = [ctypes.POINTER(PaDecodeArgs), _vp]
+        lib.pa_decode_noalloc.restype = ctypes.c_int
         lib.pa_decode_partials.argtypes = [ctypes.POINTER(PaDecodeArgs), _vp]
         lib.pa_decode_partials.restype = ctypes.c_int
         lib.pa_split_reduce.argtypes = [ctypes.POINTER(PaReduceArgs), _vp]

@@ -700,6 +700,38 @@ def paged_decode_hip(
 paged_decode_triton = paged_decode_hip
 
 
+def decode_noalloc(
+    q: torch.Tensor,
+    cache: PagedKVCache,
+    out: torch.Tensor,
+    num_splits: int = 1,
+    max_seq_len: int = 0,
+    flat_splits: int = 0,
+    sm_scale: float | None = None,
+) -> torch.Tensor:
+    """The decode through pa_decode_noalloc, which allocates nothing.
+
+    The same launch and results as `paged_decode_hip(q, cache, out=out,
+    num_splits=..., max_seq_len=..., flat_splits=...)`, but the split
+    partials live in the library's static per-GPU scratch
+    (PA_NOALLOC_SCRATCH_BYTES) instead of a torch workspace, so the call
+    makes no allocation and no host sync: for callers that cannot allocate
+    (HIP graph capture, allocation-free serving loops). `out` must be given.
+    Calls that overlap on one GPU share the scratch and race. A launch whose
+    partials do not fit raises NotImplementedError before anything runs.
+    """
+    if out is None:
+        raise ValueError("decode_noalloc writes into a caller-supplied out")
+    scale = cache.shape.softmax_scale if sm_scale is None else float(sm_scale)
+    flat = int(flat_splits or 0)
+    args = _fill_args(q, cache, out, 1 if flat else int(num_splits), scale, None, None,
+                      int(max_seq_len or 0), flat)
+    lib = _abi.load()
+    rc = _call(q.device, lib.pa_decode_noalloc, ctypes.byref(args), _stream(q.device))
+    _abi.check(rc, "pa_decode_noalloc")
+    return out
+
+
 def decode_partials(
     q: torch.Tensor,
     cache: PagedKVCache,
@@ -808,6 +840,7 @@ __all__ = [
     "paged_decode_triton",
     "pick_num_splits",
     "decode_partials",
+    "decode_noalloc",
     "split_reduce",
     "flat_merge",
     "split_count_for",
