@@ -325,7 +325,7 @@ def measure(cfg: str, args, dev, cpu: bool) -> dict:
     import torch
 
     from oracle import reference as oracle
-    from pagedattn import allocate, flat_waves_per_simd, plan_decode, plan_num_splits
+    from pagedattn import allocate, flat_waves_per_simd, plan_launch, plan_num_splits
     from pagedattn.hip_decode import (_WS, _cu_count, decode_partials, flat_merge, paged_decode_hip,
                                       split_reduce)
 
@@ -356,23 +356,28 @@ def measure(cfg: str, args, dev, cpu: bool) -> dict:
     # the workload's lengths are known here, so the planner sees them all
     # unless --splits / --flat force a launch shape
     wps = flat_waves_per_simd(wl.kv_dtype, shape.head_dim, sdt)
-    splits, _, flat = plan_decode(wl.lens, shape.num_kv_heads, shape.gqa_group, cus, wps,
-                                  kv_dtype=wl.kv_dtype, head_dim=shape.head_dim)
+    plan = plan_launch(wl.batch, 0, shape.num_kv_heads, shape.gqa_group, cus, wps,
+                       kv_dtype=wl.kv_dtype, head_dim=shape.head_dim, seq_lens=wl.lens)
+    splits, flat, cost = plan.num_splits, plan.flat_splits, plan.flat_seq_cost
     if args.flat is not None or args.splits:
         flat = int(args.flat or 0)
         splits = 1 if flat else (args.splits or
                                  plan_num_splits(wl.lens, shape.num_kv_heads, shape.gqa_group, cus)[0])
+    if args.seq_cost is not None:
+        cost = args.seq_cost
+    cost = cost if flat else 0
     out = torch.empty_like(q)
     algo = _algorithmic_bytes(cache)
     msl = max(wl.lens)
-    launch = f"flat F={flat}" if flat else ("unsplit" if splits == 1 else f"split S={splits}")
+    launch = (f"flat F={flat}" + (f" cost {cost}" if cost else "")) if flat else (
+        "unsplit" if splits == 1 else f"split S={splits}")
     _log(f"{cus} CUs, {launch}, algorithmic bytes/call={algo}")
 
     # bit stability now; parity of sampled sequences against the CPU oracle
     # after the timed regions, so that seconds of CPU work do not leave the
     # GPU idle (and clocked down) right before them
     step = lambda i: paged_decode_hip(q, caches[i % copies], out=out, num_splits=splits,
-                                      max_seq_len=msl, flat_splits=flat)
+                                      max_seq_len=msl, flat_splits=flat, flat_seq_cost=cost)
     step(0)
     first = out.clone()
     step(0)
@@ -411,7 +416,8 @@ def measure(cfg: str, args, dev, cpu: bool) -> dict:
     # the dominant kernel alone: the decode pass (partials when split)
     if flat:
         fo, fl = _WS.get_flat(wl.batch + flat, shape.num_q_heads, shape.head_dim, dev)
-        run = lambda c: decode_partials(q, c, 1, part_out=fo, part_lse=fl, flat_splits=flat, out=out)
+        run = lambda c: decode_partials(q, c, 1, part_out=fo, part_lse=fl, flat_splits=flat, out=out,
+                                        flat_seq_cost=cost)
     elif splits > 1:
         part_out, part_lse = _WS.get(wl.batch, shape.num_q_heads, splits, shape.head_dim, dev)
         run = lambda c: decode_partials(q, c, splits, part_out=part_out, part_lse=part_lse,
@@ -437,7 +443,7 @@ def measure(cfg: str, args, dev, cpu: bool) -> dict:
     merge = None
     if flat:
         run(caches[0])  # the slots of one pass
-        merge = lambda i: flat_merge(q, caches[0], flat, fo, fl, out)
+        merge = lambda i: flat_merge(q, caches[0], flat, fo, fl, out, flat_seq_cost=cost)
     elif splits > 1:
         merge = lambda i: split_reduce(part_out, part_lse, out)
     if merge is not None:
@@ -464,7 +470,8 @@ def measure(cfg: str, args, dev, cpu: bool) -> dict:
     kernel_name = "paged_decode_flat_kernel" if flat else "paged_decode_kernel"
     traffic, traffic_note = traffic_for(wl.name, kernel_name)
     res = {
-        "wl": wl, "shape": shape, "splits": splits, "flat": flat, "launch": launch, "copies": copies,
+        "wl": wl, "shape": shape, "splits": splits, "flat": flat, "seq_cost": cost, "launch": launch,
+        "copies": copies,
         "us_per_call": ms_step * 1e3, "kernel_us": kern_us, "merge_us": reduce_us, "graph_us": graph_us,
         "algo": algo, "kv_bytes": cache.bytes_read_per_decode_step(), "max_abs": max_abs, "rel": rel,
         "rows": rows, "bit_stable": bit_stable, "kernel_name": kernel_name, "traffic": traffic,
@@ -528,6 +535,8 @@ def main() -> int:
     ap.add_argument("--write-tokens", type=int, default=65536)
     ap.add_argument("--flat", type=int, default=None,
                     help="flat (work-balanced) split with this many ranges per kv head; 0 = classic")
+    ap.add_argument("--seq-cost", type=int, default=None,
+                    help="override the flat split's per-sequence charge in tiles (flat_seq_cost)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -596,6 +605,7 @@ def main() -> int:
             "seq_len_max": max(wl.lens),
             "num_splits": h["splits"],
             "flat_splits": h["flat"],
+            "flat_seq_cost": h["seq_cost"],
             "pool_copies_rotated": h["copies"],
             "parallelism": "single GPU",
         },

@@ -57,7 +57,7 @@
 extern "C" {
 #endif
 
-#define PA_ABI_VERSION 5
+#define PA_ABI_VERSION 6
 
 /* Return codes. */
 #define PA_OK 0
@@ -90,6 +90,7 @@ extern "C" {
  * one pass. */
 #define PA_MAX_SPLITS 4096
 #define PA_MAX_FLAT_SPLITS 65536
+#define PA_MAX_FLAT_SEQ_COST 64
 #define PA_MAX_GROUP 16
 
 typedef struct pa_decode_args {
@@ -144,6 +145,13 @@ typedef struct pa_decode_args {
    * [batch + F, num_q_heads] with stride_lb / stride_lh; stride_ps is unused.
    * Every wave scans seq_lens once (batch / 64 loads per lane). */
   int32_t flat_splits;
+  /* Flat split only (also an addition): tiles of weight charged to each
+   * non-empty sequence when the ranges are cut, 0 .. PA_MAX_FLAT_SEQ_COST.
+   * 0: equal tile counts. c > 0: sequence b weighs c + ceil(T_b / 32) and the
+   * ranges take equal weight, so a range that starts several sequences
+   * (each start costs a wave about one tile of time) holds fewer tiles;
+   * suits ragged batches. pa_flat_merge must be given the same value. */
+  int32_t flat_seq_cost;
 } pa_decode_args;
 
 typedef struct pa_reduce_args {

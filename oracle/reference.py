@@ -197,29 +197,36 @@ def split_partials(
     return part, lse
 
 
-def flat_segments(seq_lens, flat_splits: int, align: int = 32) -> tuple[list[tuple[int, int, int, int]], int]:
+def flat_segments(seq_lens, flat_splits: int, align: int = 32,
+                  seq_cost: int = 0) -> tuple[list[tuple[int, int, int, int]], int]:
     """The flat split's work list and range size: ([(j, b, lo, hi)], per).
 
     No counterpart in the reference: the HIP build's work-balanced split.
-    Sequence b owns flat tiles [cu_b, cu_b + n_b), n_b = ceil(T_b / align),
-    in batch order; range j covers flat tiles [j * per, (j + 1) * per) with
-    per = max(1, ceil(total / flat_splits)). Each (j, b, lo, hi) is the token
-    range [lo, hi) of sequence b that range j holds, in order.
+    Sequence b has n_b = ceil(T_b / align) tiles and, when non-empty, weighs
+    n_b + seq_cost; sequences are laid end to end in batch order, so b spans
+    weights [cw_b, cw_b + seq_cost + n_b) and its tile k sits at weight
+    cw_b + seq_cost + k. Range j covers weights [j * per, (j + 1) * per) with
+    per = max(1, ceil(W / flat_splits)) over the total weight W and holds the
+    tiles whose weights fall inside. Each (j, b, lo, hi) is the token range
+    [lo, hi) of sequence b that range j holds, in order. seq_cost = 0 is the
+    plain split of the tiles into equal ranges.
     """
     lens = [max(0, int(t)) for t in seq_lens]
     tiles = [-(-t // align) for t in lens]
-    total = sum(tiles)
+    weights = [n + seq_cost if n else 0 for n in tiles]
+    total = sum(weights)
     per = max(1, -(-total // flat_splits))
     segs = []
-    cu = 0
+    cw = 0
     for b, (t, n) in enumerate(zip(lens, tiles)):
-        f = cu
-        while f < cu + n:
+        first = cw + seq_cost  # weight of tile 0
+        f = first
+        while f < first + n:
             j = f // per
-            end = min(cu + n, (j + 1) * per)
-            segs.append((j, b, (f - cu) * align, min((end - cu) * align, t)))
+            end = min(first + n, (j + 1) * per)
+            segs.append((j, b, (f - first) * align, min((end - first) * align, t)))
             f = end
-        cu += n
+        cw += weights[b]
     return segs, per
 
 
@@ -229,6 +236,7 @@ def flat_partials(
     flat_splits: int,
     align: int = 32,
     sm_scale: float | None = None,
+    seq_cost: int = 0,
 ) -> tuple[torch.Tensor, torch.Tensor, list[bool]]:
     """The flat decode pass: (part [B + F, Hq, D], lse [B + F, Hq], whole [B]).
 
@@ -245,7 +253,7 @@ def flat_partials(
     v = v.float()
     scale = _softmax_scale(cache, sm_scale) * math.log2(math.e)
     lens = cache.seq_lens.cpu().long().tolist()
-    segs, _ = flat_segments(lens, flat_splits, align)
+    segs, _ = flat_segments(lens, flat_splits, align, seq_cost)
     part = torch.zeros((b + flat_splits, hq, d), dtype=torch.float32)
     lse = torch.full((b + flat_splits, hq), float("-inf"), dtype=torch.float32)
     count = [0] * b

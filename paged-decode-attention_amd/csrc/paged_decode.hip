@@ -109,6 +109,7 @@ struct KParams {
   int32_t hkv, group, head_tiles, num_splits, num_blocks, max_blocks, log2_page, max_seq_len;
   int32_t batch, max_tokens;  // max_tokens = max_blocks << log2_page
   int32_t flat_splits;        // > 0: the flat (work-balanced) split
+  int32_t flat_cost;          // flat split: tiles charged per non-empty sequence
   int64_t sqb, sqh;          // elements
   int64_t skn, skt, skh;     // bytes
   int64_t ssn, sst;          // bytes
@@ -129,6 +130,7 @@ struct RParams {
   int32_t max_tokens, max_seq_len;  // AUTO and FLAT merges only
   int32_t num_heads, num_splits;    // FLAT: num_splits = flat splits
   int32_t batch;                    // FLAT only
+  int32_t flat_cost;                // FLAT only: tiles charged per non-empty sequence
   int64_t spb, sph, sps, slb, slh, sob, soh;  // elements
 };
 
@@ -994,6 +996,16 @@ paged_decode_kernel(const KParams p) {
 // Slots are unique: if range j - 1 reached sequence b + 1, sequence b ended
 // before range j began. The merge (split_reduce_kernel<D, kMergeFlat>)
 // derives the same ranges from seq_lens and folds slots b + j0 .. b + j1.
+//
+// Equal tile counts are not equal times when a range crosses sequences: each
+// sequence a wave starts costs it a new q, a store and a pipeline restart
+// (about one fp8 tile at head_dim 128). With flat_cost = c > 0 every
+// non-empty sequence is charged c tiles of weight ahead of its first tile:
+// sequence b spans weights [cw_b, cw_b + c + n_b), its tile k sits at weight
+// cw_b + c + k, and range j takes the tiles whose weights fall in
+// [j * per, (j + 1) * per), per = ceil(W / F) over the total weight W. The
+// ranges stay contiguous in sequence order (the slot rule above holds); a
+// range that covers charges only holds no tiles. c = 0 is the plain split.
 // ----------------------------------------------------------------------------
 
 // Tiles of sequence b (its length clamped to the block table).
@@ -1118,6 +1130,80 @@ __device__ __forceinline__ SeqCursor flat_locate(const ro_i32 *seq_lens, int bat
   return cur;
 }
 
+// Weight of a sequence of `tiles` tiles under a charge of `cost` tiles per
+// non-empty sequence.
+__device__ __forceinline__ int seq_weight(int tiles, int cost) { return tiles > 0 ? tiles + cost : 0; }
+
+// Range j of F under a charge of cost > 0 tiles per sequence: its first tile
+// (the returned cursor) and its tile count `n` (0: the range holds charges
+// only, or lies past the end). Per lane: a = the sequence's tiles whose
+// weights lie below the range, e = those below its end; n = sum(e - a).
+__device__ __forceinline__ SeqCursor flat_locate_weighted(const ro_i32 *seq_lens, int batch,
+                                                          int max_tokens, int F, int j, int cost,
+                                                          int lane, int &n) {
+  SeqCursor cur = {0, 0, 0, 0};
+  n = 0;
+  if (batch <= 64) {  // one chunk: one scan gives the weights, the range and its start
+    const int len = lane < batch ? max(0, min(seq_lens[lane], max_tokens)) : 0;
+    const int t = len_tiles(len);
+    const int w = seq_weight(t, cost);
+    const int incl = wave_incl_scan(w, lane);
+    const int W = __builtin_amdgcn_readlane(incl, 63);
+    const int per = max(1, (W + F - 1) / F);
+    const int r0 = j * per;
+    if (r0 >= W) return cur;
+    const int r1 = min(W, r0 + per);
+    const int first = incl - w + cost;  // weight of the sequence's tile 0
+    const int a = min(max(r0 - first, 0), t), e = min(max(r1 - first, 0), t);
+    n = __builtin_amdgcn_readfirstlane(wave_sum(e - a));
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(a < t);
+    if (n == 0 || hit == 0) {
+      n = 0;
+      return cur;
+    }
+    const int l = __builtin_ctzll(hit);
+    cur.b = l;
+    cur.t = __builtin_amdgcn_readlane(a, l);
+    cur.len = __builtin_amdgcn_readlane(len, l);
+    cur.tiles = (cur.len + kSplitAlign - 1) / kSplitAlign;
+    return cur;
+  }
+  // total weight, then the range's tiles before and inside it, chunk by chunk
+  int W = 0;
+  for (int base = 0; base < batch; base += 64 * kLenChunks) {
+    int len[kLenChunks];
+    load_len_chunks(seq_lens, batch, max_tokens, base, lane, len);
+    int s = 0;
+#pragma unroll
+    for (int k = 0; k < kLenChunks; ++k) s += seq_weight(len_tiles(len[k]), cost);
+    W += wave_sum(s);
+  }
+  W = __builtin_amdgcn_readfirstlane(W);
+  const int per = max(1, (W + F - 1) / F);
+  const int r0 = j * per;
+  if (r0 >= W) return cur;
+  const int r1 = min(W, r0 + per);
+  int run = 0, start = 0, cnt = 0;  // run: weight of the sequences before this chunk
+  for (int base = 0; base < batch && run < r1; base += 64 * kLenChunks) {
+    int len[kLenChunks];
+    load_len_chunks(seq_lens, batch, max_tokens, base, lane, len);
+#pragma unroll
+    for (int k = 0; k < kLenChunks; ++k) {
+      const int t = len_tiles(len[k]);
+      const int w = seq_weight(t, cost);
+      const int incl = wave_incl_scan(w, lane) + run;
+      const int first = incl - w + cost;
+      const int a = min(max(r0 - first, 0), t), e = min(max(r1 - first, 0), t);
+      start += wave_sum(a);
+      cnt += wave_sum(e - a);
+      run = __builtin_amdgcn_readlane(incl, 63);
+    }
+  }
+  n = __builtin_amdgcn_readfirstlane(cnt);
+  if (n == 0) return cur;
+  return flat_locate(seq_lens, batch, max_tokens, __builtin_amdgcn_readfirstlane(start), lane, -1);
+}
+
 // Step to the next flat tile. Only called while the range has another tile,
 // so a non-empty sequence follows; the batch bound only guards the reads.
 __device__ __forceinline__ void cursor_next(SeqCursor &cur, const ro_i32 *seq_lens, int batch,
@@ -1173,15 +1259,23 @@ paged_decode_flat_kernel(const KParams p) {
   const int qh0 = kvh * p.group + ht * 16;
   const int nh = min(16, p.group - ht * 16);
 
-  int len0 = 0;
-  const int total = flat_total(ro(p.seq_lens), p.batch, p.max_tokens, lane, len0);
-  const int per = max(1, (total + p.flat_splits - 1) / p.flat_splits);
-  const int r0 = j * per;
-  if (r0 >= total) return;
-  const int n = min(per, total - r0);  // this wave's tiles
-
-  // compute cursor (one pass over seq_lens when the batch fits one wave)
-  SeqCursor cc = flat_locate(ro(p.seq_lens), p.batch, p.max_tokens, r0, lane, p.batch <= 64 ? len0 : -1);
+  // compute cursor at the range's first tile, and the range's tile count
+  // (one pass over seq_lens when the batch fits one wave)
+  SeqCursor cc;
+  int n;  // this wave's tiles
+  if (p.flat_cost == 0) {
+    int len0 = 0;
+    const int total = flat_total(ro(p.seq_lens), p.batch, p.max_tokens, lane, len0);
+    const int per = max(1, (total + p.flat_splits - 1) / p.flat_splits);
+    const int r0 = j * per;
+    if (r0 >= total) return;
+    n = min(per, total - r0);
+    cc = flat_locate(ro(p.seq_lens), p.batch, p.max_tokens, r0, lane, p.batch <= 64 ? len0 : -1);
+  } else {
+    cc = flat_locate_weighted(ro(p.seq_lens), p.batch, p.max_tokens, p.flat_splits, j, p.flat_cost,
+                              lane, n);
+    if (n == 0) return;
+  }
   SeqCursor lc = cc;                                                        // load cursor
   int seg_t0 = cc.t;  // first tile of the current segment
 
@@ -1329,13 +1423,15 @@ __global__ void __launch_bounds__(kMergeWaves * 64) split_reduce_kernel(const RP
     S = split_range(seq_len, p.num_splits, p.max_seq_len, 0).n;
     if (S <= 1) return;
   } else if (KIND == kMergeFlat) {
-    // the decode's ranges: per = ceil(total / F) flat tiles each
+    // the decode's ranges: per = ceil(total / F) of weight each, where a
+    // non-empty sequence weighs its tiles plus flat_cost
     const int nt = seq_tiles(ro(p.seq_lens), b, p.max_tokens);
-    int total = 0, cu = 0;
+    const int cost = p.flat_cost;
+    int total = 0, cu = 0;  // all weight, weight before sequence b
     if (p.batch <= 64) {  // one chunk
       const int t = lane < p.batch ? seq_tiles(ro(p.seq_lens), lane, p.max_tokens) : 0;
-      total = wave_sum(t);
-      cu = wave_sum(lane < b ? t : 0);
+      total = wave_sum(seq_weight(t, cost));
+      cu = wave_sum(lane < b ? seq_weight(t, cost) : 0);
     }
     for (int base = 0; base < p.batch && p.batch > 64; base += 64 * kLenChunks) {
       int len[kLenChunks];
@@ -1343,9 +1439,9 @@ __global__ void __launch_bounds__(kMergeWaves * 64) split_reduce_kernel(const RP
       int t = 0, tb = 0;
 #pragma unroll
       for (int k = 0; k < kLenChunks; ++k) {
-        const int tk = len_tiles(len[k]);
-        t += tk;
-        tb += base + 64 * k + lane < b ? tk : 0;
+        const int wk = seq_weight(len_tiles(len[k]), cost);
+        t += wk;
+        tb += base + 64 * k + lane < b ? wk : 0;
       }
       total += wave_sum(t);
       cu += wave_sum(tb);
@@ -1353,7 +1449,8 @@ __global__ void __launch_bounds__(kMergeWaves * 64) split_reduce_kernel(const RP
     S = 0;  // empty sequence: the merge below writes zeros
     if (nt > 0) {
       const int per = max(1, (total + p.num_splits - 1) / p.num_splits);
-      const int j0 = cu / per, j1 = (cu + nt - 1) / per;
+      const int first = cu + cost;  // weight of b's tile 0
+      const int j0 = first / per, j1 = (first + nt - 1) / per;
       if (j0 == j1) return;
       S = j1 - j0 + 1;
       lse = p.part_lse + (int64_t)(b + j0) * p.slb + (int64_t)h * p.slh;
@@ -1525,6 +1622,8 @@ int build_params(const pa_decode_args *a, bool need_partials, KParams *kp) {
   }
   if (a->flat_splits < 0 || a->flat_splits > PA_MAX_FLAT_SPLITS)
     return fail(PA_ERR_INVALID, "flat_splits %d not in [0, %d]", a->flat_splits, PA_MAX_FLAT_SPLITS);
+  if (a->flat_seq_cost < 0 || a->flat_seq_cost > PA_MAX_FLAT_SEQ_COST)
+    return fail(PA_ERR_INVALID, "flat_seq_cost %d not in [0, %d]", a->flat_seq_cost, PA_MAX_FLAT_SEQ_COST);
   if (a->flat_splits > 0) need_partials = true;
   if (need_partials && (!a->part_out || !a->part_lse))
     return fail(PA_ERR_INVALID, "num_splits > 1 / flat_splits > 0 need part_out and part_lse");
@@ -1567,7 +1666,7 @@ int build_params(const pa_decode_args *a, bool need_partials, KParams *kp) {
   if (a->flat_splits > 0) {
     // flat tile counts, range starts and slot indices are 32-bit in the kernel
     const int64_t seq_tiles_max = ((int64_t)a->max_blocks * a->block_size + kSplitAlign - 1) / kSplitAlign;
-    if ((int64_t)a->batch * seq_tiles_max + a->flat_splits > 0x7fffffff)
+    if ((int64_t)a->batch * (seq_tiles_max + a->flat_seq_cost) + a->flat_splits > 0x7fffffff)
       return fail(PA_ERR_UNSUPPORTED, "batch * max tiles per sequence too large for the flat split");
     if ((int64_t)a->num_kv_heads * head_tiles * a->flat_splits + kFlatWaves > 0x7fffffff)
       return fail(PA_ERR_UNSUPPORTED, "flat split grid too large");
@@ -1595,6 +1694,7 @@ int build_params(const pa_decode_args *a, bool need_partials, KParams *kp) {
   k.batch = a->batch;
   k.max_tokens = a->max_blocks << k.log2_page;
   k.flat_splits = a->flat_splits;
+  k.flat_cost = a->flat_splits > 0 ? a->flat_seq_cost : 0;
   k.sqb = a->stride_qb;
   k.sqh = a->stride_qh;
   k.skn = a->stride_kn * elem;
@@ -1682,6 +1782,7 @@ int check_reduce(const pa_reduce_args *r, RParams *rp) {
   rp->max_tokens = 0;
   rp->max_seq_len = 0;
   rp->batch = r->batch;
+  rp->flat_cost = 0;
   rp->num_heads = r->num_heads;
   rp->num_splits = r->num_splits;
   rp->spb = r->stride_pb;
@@ -1804,7 +1905,10 @@ int pa_decode(const pa_decode_args *a, void *stream) {
     rp.seq_lens = a->seq_lens;
     rp.max_tokens = k.max_tokens;
     rp.max_seq_len = a->max_seq_len;
-    if (flat) rp.num_splits = a->flat_splits;
+    if (flat) {
+      rp.num_splits = a->flat_splits;
+      rp.flat_cost = a->flat_seq_cost;
+    }
   }
   if (a->batch == 0) return ok();
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -1884,6 +1988,7 @@ int pa_flat_merge(const pa_decode_args *a, void *stream) {
   rp.seq_lens = a->seq_lens;
   rp.max_tokens = k.max_tokens;
   rp.num_splits = a->flat_splits;
+  rp.flat_cost = a->flat_seq_cost;
   if (a->batch == 0) return ok();
   hipError_t e = launch_reduce<kMergeFlat>(rp, a->batch, a->head_dim, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(PA_ERR_HIP, "reduce launch failed: %s", hipGetErrorString(e));

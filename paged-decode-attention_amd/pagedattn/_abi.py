@@ -12,7 +12,7 @@ import os
 import pathlib
 import threading
 
-PA_ABI_VERSION = 5
+PA_ABI_VERSION = 6
 
 PA_OK = 0
 PA_ERR_INVALID = -1
@@ -33,6 +33,7 @@ PA_IO_BF16 = 1
 
 PA_MAX_SPLITS = 4096
 PA_MAX_FLAT_SPLITS = 65536
+PA_MAX_FLAT_SEQ_COST = 64
 PA_NOALLOC_SCRATCH_BYTES = 32 << 20
 PA_MAX_GROUP = 16
 
@@ -97,6 +98,7 @@ class PaDecodeArgs(ctypes.Structure):
         ("io_dtype", _i32),
         ("sm_scale", ctypes.c_float),
         ("flat_splits", _i32),
+        ("flat_seq_cost", _i32),
     ]
 
 

@@ -70,6 +70,15 @@ FLAT_WAVES_PER_SIMD = 1
 # 107.1 / 95.0, fp16 97.1 / 92.4; Qwen2.5 B = 256, T = 2048 41.7 / 38.0.
 FLAT_WAVES_PER_SIMD_KV = {"int8": 2}
 MIN_FLAT_TILES_PER_WAVE = 4
+# Tiles of weight the flat split charges each sequence of a ragged batch
+# (flat_seq_cost): a wave that starts a sequence loads a new q, stores a
+# result and restarts its tile pipeline, about 0.9 us against 1.0 us per fp8
+# tile at head_dim 128 (per-wave timestamps, Llama-3-8B shape, C3's lengths:
+# ranges of 27 tiles ended 2.7 us later when they held 4 sequences than when
+# they held 1). Nearly uniform batches keep 0: their ranges then fall on
+# sequence boundaries or cut every sequence alike, and a charge would only
+# unbalance them.
+RAGGED_FLAT_SEQ_COST = 1
 # A single sequence up to this many tiles takes the classic split: cut into
 # one chunk per CU it merges 32 partials per head, the flat split 128 (graph-
 # timed whole calls, classic against flat: T = 16384 17.9 / 21.0 us, 32768
@@ -261,18 +270,20 @@ class LaunchPlan:
     says whether its merge pass has work (False when every sequence lies
     inside one range, so the decode pass writes all of `out`).
     flat_splits == 0: the classic kernel with `num_splits` per-sequence
-    splits (1 = unsplit), chunked from `max_seq_len`.
+    splits (1 = unsplit), chunked from `max_seq_len`. `flat_seq_cost`: the
+    tiles of weight the flat split charges each sequence (0 = equal tiles).
     """
 
     num_splits: int
     max_seq_len: int
     flat_splits: int
     merge: bool = True
+    flat_seq_cost: int = 0
 
     def launch_kwargs(self) -> dict:
         """Keywords of `paged_decode_hip` that select this launch."""
         if self.flat_splits:
-            return {"flat_splits": self.flat_splits}
+            return {"flat_splits": self.flat_splits, "flat_seq_cost": self.flat_seq_cost}
         return {"num_splits": self.num_splits, "max_seq_len": self.max_seq_len}
 
 
@@ -299,6 +310,8 @@ def plan_launch(batch: int, max_seq_len: int, num_kv_heads: int, group: int, sm_
             unless the flat split needs no merge either (`flat_needs_merge`);
       * otherwise the classic split (`plan_num_splits`), on the known
         lengths or on `batch` sequences of `max_seq_len` tokens.
+    A flat plan charges each sequence RAGGED_FLAT_SEQ_COST tiles when the
+    lengths are known and not nearly uniform, else nothing.
     """
     cus = max(1, sm_count)
     known = seq_lens is not None
@@ -315,7 +328,8 @@ def plan_launch(batch: int, max_seq_len: int, num_kv_heads: int, group: int, sm_
                and not (batch == 1 and _tiles(tmax) <= SINGLE_SEQ_SPLIT_MAX_TILES))
     if flat_ok:
         fills = known and _fills_unsplit(lens, num_kv_heads, group, cus)
-        merge = flat_needs_merge(lens, flat) if known else True
+        cost = RAGGED_FLAT_SEQ_COST if known and not _nearly_uniform(lens) else 0
+        merge = flat_needs_merge(lens, flat, seq_cost=cost) if known else True
         if kv_dtype is not None and head_dim is not None:
             if short_batch_runs_unsplit(batch, tmax, num_kv_heads, group, cus, kv_dtype,
                                         uniform=fills):
@@ -325,7 +339,7 @@ def plan_launch(batch: int, max_seq_len: int, num_kv_heads: int, group: int, sm_
             limit = UNSPLIT_MAX_KV_BYTES_PER_CU.get(kv_dtype, 0) * cus
             if fills and kv_bytes <= limit and merge:
                 return LaunchPlan(1, tmax, 0)
-        return LaunchPlan(1, tmax, flat, merge)
+        return LaunchPlan(1, tmax, flat, merge, cost)
     # the classic split, planned on the lengths (unknown: every sequence as
     # long as the longest, which sizes the chunks for the worst case)
     splits, tmax = plan_num_splits(lens if known else [tmax] * batch, num_kv_heads, group, cus)
@@ -343,7 +357,8 @@ def plan_decode(seq_lens, num_kv_heads: int, group: int, sm_count: int,
     return p.num_splits, p.max_seq_len, p.flat_splits
 
 
-def flat_needs_merge(seq_lens, flat_splits: int, max_tokens: int | None = None) -> bool:
+def flat_needs_merge(seq_lens, flat_splits: int, max_tokens: int | None = None,
+                     seq_cost: int = 0) -> bool:
     """Whether a flat decode over these lengths leaves work to its merge pass.
 
     It does when a range boundary cuts a sequence (its pieces are partials)
@@ -351,21 +366,25 @@ def flat_needs_merge(seq_lens, flat_splits: int, max_tokens: int | None = None) 
     sequence lies inside one range and the decode pass writes all of `out`
     itself, as for a uniform batch whose length in tiles times the batch
     divides evenly among the ranges. Lengths are clamped to `max_tokens` (the
-    block table's capacity), as the kernels clamp them.
+    block table's capacity), as the kernels clamp them. `seq_cost` is the
+    launch's flat_seq_cost: a non-empty sequence weighs its tiles plus
+    `seq_cost`, and the ranges take equal weight.
     """
     lens = [max(0, int(t)) for t in seq_lens]
     if max_tokens is not None:
         lens = [min(t, max_tokens) for t in lens]
     tiles = [_tiles(t) for t in lens]
-    total = sum(tiles)
+    weights = [n + seq_cost if n else 0 for n in tiles]
+    total = sum(weights)
     if total == 0 or flat_splits <= 0:
         return True
     per = max(1, -(-total // flat_splits))
-    cu = 0
-    for n in tiles:
-        if n == 0 or cu // per != (cu + n - 1) // per:
+    cw = 0
+    for n, w in zip(tiles, weights):
+        first = cw + seq_cost  # weight of the sequence's tile 0
+        if n == 0 or first // per != (first + n - 1) // per:
             return True
-        cu += n
+        cw += w
     return False
 
 
@@ -509,6 +528,7 @@ def _fill_args(
     part_lse: torch.Tensor | None,
     max_seq_len: int = 0,
     flat_splits: int = 0,
+    flat_seq_cost: int = 0,
 ) -> _abi.PaDecodeArgs:
     b, hq, d = q.shape
     shape = cache.shape
@@ -585,7 +605,8 @@ def _fill_args(
         int(max_seq_len),
         qst[0], qst[1], kst[0], kst[1], kst[2], sst[0], sst[1], ost[0], ost[1],
         pst[0], pst[1], pst[2], lst[0], lst[1], btst[0],
-        _KV_CODE[kv_dtype], scale_code, _IO_CODE[q.dtype], sm_scale, int(flat_splits))
+        _KV_CODE[kv_dtype], scale_code, _IO_CODE[q.dtype], sm_scale, int(flat_splits),
+        int(flat_seq_cost))
 
 
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
@@ -620,6 +641,7 @@ def paged_decode_hip(
     sm_scale: float | None = None,
     max_seq_len: int | None = None,
     flat_splits: int | None = None,
+    flat_seq_cost: int | None = None,
 ) -> torch.Tensor:
     """Paged GQA decode attention. q: [B, Hq, D] fp16|bf16 -> [B, Hq, D] in q's dtype.
 
@@ -643,7 +665,10 @@ def paged_decode_hip(
     into `flat_splits` equal ranges, one wave each, so ragged lengths cost no
     tail; `num_splits` and `max_seq_len` are then unused. It needs no
     host-side lengths, so a serving loop can pass a fixed value
-    (`flat_splits_for`).
+    (`flat_splits_for`). `flat_seq_cost` (0 when not given with
+    `flat_splits`) charges each sequence that many tiles of weight when the
+    ranges are cut, which balances ranges that start several sequences
+    (`plan_launch` sets RAGGED_FLAT_SEQ_COST for ragged batches).
     """
     del per_page_bt, num_warps, num_stages
     b, hq, d = q.shape
@@ -662,6 +687,7 @@ def paged_decode_hip(
     merge = True  # a flat decode runs its merge pass
     if flat_splits:
         num_splits = 1
+        flat_seq_cost = int(flat_seq_cost or 0)
     elif num_splits is None:
         # the lengths come to the host in the one sync the reference also makes
         lens = cache.seq_lens.tolist()
@@ -669,10 +695,13 @@ def paged_decode_hip(
         plan = plan_launch(b, 0, hkv, group, _cu_count(q.device), wps, kv_dtype=cache.kv_dtype,
                            head_dim=d, seq_lens=lens)
         num_splits, flat_splits = plan.num_splits, plan.flat_splits
+        if flat_seq_cost is None:
+            flat_seq_cost = plan.flat_seq_cost
         if max_seq_len is None:
             max_seq_len = plan.max_seq_len
         if flat_splits:
-            merge = flat_needs_merge(lens, flat_splits, cache.block_table.shape[1] * cache.block_size)
+            merge = flat_needs_merge(lens, flat_splits, cache.block_table.shape[1] * cache.block_size,
+                                     int(flat_seq_cost))
     num_splits = int(num_splits)
     scale = shape.softmax_scale if sm_scale is None else float(sm_scale)
 
@@ -683,7 +712,8 @@ def paged_decode_hip(
         part_out, part_lse = _WS.get_flat(b + flat, hq, d, q.device)
     elif num_splits > 1:
         part_out, part_lse = _WS.get(b, hq, num_splits, d, q.device)
-    args = _fill_args(q, cache, out, num_splits, scale, part_out, part_lse, max_seq_len or 0, flat)
+    args = _fill_args(q, cache, out, num_splits, scale, part_out, part_lse, max_seq_len or 0, flat,
+                      int(flat_seq_cost or 0) if flat else 0)
     lib = _abi.load()
     if flat > 0 and not merge:
         # every sequence inside one range: the decode pass writes all of out
@@ -708,11 +738,12 @@ def decode_noalloc(
     max_seq_len: int = 0,
     flat_splits: int = 0,
     sm_scale: float | None = None,
+    flat_seq_cost: int = 0,
 ) -> torch.Tensor:
     """The decode through pa_decode_noalloc, which allocates nothing.
 
     The same launch and results as `paged_decode_hip(q, cache, out=out,
-    num_splits=..., max_seq_len=..., flat_splits=...)`, but the split
+    num_splits=..., max_seq_len=..., flat_splits=..., flat_seq_cost=...)`, but the split
     partials live in the library's static per-GPU scratch
     (PA_NOALLOC_SCRATCH_BYTES) instead of a torch workspace, so the call
     makes no allocation and no host sync: for callers that cannot allocate
@@ -725,7 +756,7 @@ def decode_noalloc(
     scale = cache.shape.softmax_scale if sm_scale is None else float(sm_scale)
     flat = int(flat_splits or 0)
     args = _fill_args(q, cache, out, 1 if flat else int(num_splits), scale, None, None,
-                      int(max_seq_len or 0), flat)
+                      int(max_seq_len or 0), flat, int(flat_seq_cost or 0) if flat else 0)
     lib = _abi.load()
     rc = _call(q.device, lib.pa_decode_noalloc, ctypes.byref(args), _stream(q.device))
     _abi.check(rc, "pa_decode_noalloc")
@@ -742,6 +773,7 @@ def decode_partials(
     max_seq_len: int = 0,
     flat_splits: int = 0,
     out: torch.Tensor | None = None,
+    flat_seq_cost: int = 0,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Run only the decode pass; returns (part_out [B,Hq,S,D], part_lse [B,Hq,S]).
 
@@ -750,7 +782,8 @@ def decode_partials(
     of the reference's split epilogue (triton_decode.py:169-188).
     With `flat_splits` = F > 0 it is the flat decode pass: the partials are
     slots [B + F, Hq, D] / [B + F, Hq], and sequences that one wave range
-    holds whole are written to `out`.
+    holds whole are written to `out`; `flat_seq_cost` as for
+    `paged_decode_hip`.
     """
     b, hq, d = q.shape
     scale = cache.shape.softmax_scale if sm_scale is None else float(sm_scale)
@@ -767,7 +800,8 @@ def decode_partials(
     if out is None:
         out = torch.empty((b, hq, d), dtype=q.dtype, device=q.device)
     _check_partials(q.device, part_out, part_lse, b, hq, d, num_splits, flat_splits)
-    args = _fill_args(q, cache, out, num_splits, scale, part_out, part_lse, max_seq_len, flat_splits)
+    args = _fill_args(q, cache, out, num_splits, scale, part_out, part_lse, max_seq_len, flat_splits,
+                      flat_seq_cost if flat_splits > 0 else 0)
     lib = _abi.load()
     rc = _call(q.device, lib.pa_decode_partials, ctypes.byref(args), _stream(q.device))
     _abi.check(rc, "pa_decode_partials")
@@ -782,16 +816,18 @@ def flat_merge(
     part_lse: torch.Tensor,
     out: torch.Tensor,
     sm_scale: float | None = None,
+    flat_seq_cost: int = 0,
 ) -> torch.Tensor:
     """The flat split's merge pass alone: after `decode_partials(...,
-    flat_splits=F, out=out)` with the same arguments, folds the slots into
-    `out` (the pair equals `paged_decode_hip(..., flat_splits=F)`)."""
+    flat_splits=F, out=out, flat_seq_cost=c)` with the same arguments, folds
+    the slots into `out` (the pair equals `paged_decode_hip(...,
+    flat_splits=F, flat_seq_cost=c)`)."""
     if flat_splits <= 0:
         raise ValueError("flat_merge needs flat_splits > 0")
     scale = cache.shape.softmax_scale if sm_scale is None else float(sm_scale)
     b, hq, d = q.shape
     _check_partials(q.device, part_out, part_lse, b, hq, d, 1, flat_splits)
-    args = _fill_args(q, cache, out, 1, scale, part_out, part_lse, 0, flat_splits)
+    args = _fill_args(q, cache, out, 1, scale, part_out, part_lse, 0, flat_splits, flat_seq_cost)
     lib = _abi.load()
     rc = _call(q.device, lib.pa_flat_merge, ctypes.byref(args), _stream(q.device))
     _abi.check(rc, "pa_flat_merge")

@@ -7,7 +7,9 @@ decode pass to the oracle's restatement of the same ranges
 (oracle.flat_partials). Cases cover ranges that cut sequences, sequences
 inside one range, empty and 1-token sequences, more ranges than tiles, one
 range for the whole batch, GQA groups above 16, every KV dtype and page
-sizes above 16.
+sizes above 16. The weighted ranges (flat_seq_cost > 0: each sequence
+charged that many tiles of weight) are held to the same bar, including
+ranges that cover charges only and batches above one wave.
 """
 
 from __future__ import annotations
@@ -34,16 +36,16 @@ def _case(shape, lens, kv_dtype="fp16", block_size=16, seed=0, scale_dtype=torch
     return q, c
 
 
-def _check(q, c, flat, tol=ABS_TOL):
+def _check(q, c, flat, tol=ABS_TOL, seq_cost=0):
     # the reference's BLOCK_N rule: a multiple of the page size
-    got = paged_decode_hip(q, c, flat_splits=flat, block_n=max(64, c.block_size))
+    got = paged_decode_hip(q, c, flat_splits=flat, block_n=max(64, c.block_size), flat_seq_cost=seq_cost)
     torch.cuda.synchronize()
     want = oracle.reference_decode(q, c, out_dtype=torch.float32)
     lens = c.seq_lens.cpu().tolist()
     live = [b for b, t in enumerate(lens) if t > 0]
     dead = [b for b, t in enumerate(lens) if t == 0]
     err = max_abs(got[live], want[live]) if live else 0.0
-    print(f"flat={flat} lens={lens[:8]} max_abs={err:.2e}")
+    print(f"flat={flat} cost={seq_cost} lens={lens[:8]} max_abs={err:.2e}")
     assert err < tol
     if dead:
         assert torch.equal(got[dead].float().cpu(), torch.zeros_like(want[dead]))
@@ -54,6 +56,30 @@ def _check(q, c, flat, tol=ABS_TOL):
 def test_flat_ragged_fp16(flat):
     q, c = _case(LLAMA3_8B, RAGGED, seed=1)
     _check(q, c, flat)
+
+
+@pytest.mark.parametrize("seq_cost", [1, 3])
+@pytest.mark.parametrize("flat", [2, 7, 64, 1000])
+def test_flat_seq_cost_ragged(flat, seq_cost):
+    q, c = _case(LLAMA3_8B, RAGGED, seed=1)
+    _check(q, c, flat, seq_cost=seq_cost)
+
+
+@pytest.mark.parametrize("kv_dtype,scale_dtype", [("fp8_e5m2", torch.float16), ("int8", torch.float32)])
+def test_flat_seq_cost_kv_dtypes(kv_dtype, scale_dtype):
+    q, c = _case(LLAMA3_8B, RAGGED, kv_dtype=kv_dtype, seed=2, scale_dtype=scale_dtype)
+    _check(q, c, 96, seq_cost=1)
+
+
+def test_flat_seq_cost_ranges_of_charges_only():
+    """Weights [4, 4] over 8 ranges of 1: six ranges cover charges only and
+    hold no tiles; the two sequences are still written whole."""
+    q, c = _case(ModelShape(8, 8, 64, "mha"), [32, 32], seed=20)
+    _check(q, c, 8, seq_cost=3)
+    q, c = _case(LLAMA3_8B, [0, 0, 0], seed=5)
+    got = paged_decode_hip(q, c, flat_splits=8, flat_seq_cost=2)
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu(), torch.zeros_like(got.cpu()))
 
 
 @pytest.mark.parametrize("kv_dtype,scale_dtype", [("fp8_e5m2", torch.float16), ("int8", torch.float16),
@@ -113,8 +139,8 @@ def test_flat_bit_stable_and_matches_classic_split():
     assert max_abs(a.float(), classic.float().cpu()) < ABS_TOL
 
 
-@pytest.mark.parametrize("flat", [3, 16])
-def test_flat_partial_slots_match_oracle(flat):
+@pytest.mark.parametrize("flat,seq_cost", [(3, 0), (16, 0), (3, 1), (16, 2)])
+def test_flat_partial_slots_match_oracle(flat, seq_cost):
     """The decode pass alone: every slot a range writes equals the oracle's
     partial of the same token range, and sequences held by one range are
     already final in `out`."""
@@ -124,10 +150,11 @@ def test_flat_partial_slots_match_oracle(flat):
     part = torch.full((b + flat, hq, d), float("nan"), device="cuda")
     lse = torch.full((b + flat, hq), float("nan"), device="cuda")
     out = torch.zeros_like(q)
-    decode_partials(q, c, 1, part_out=part, part_lse=lse, flat_splits=flat, out=out)
+    decode_partials(q, c, 1, part_out=part, part_lse=lse, flat_splits=flat, out=out,
+                    flat_seq_cost=seq_cost)
     torch.cuda.synchronize()
-    opart, olse, whole = oracle.flat_partials(q, c, flat)
-    segs, _ = oracle.flat_segments(lens, flat)
+    opart, olse, whole = oracle.flat_partials(q, c, flat, seq_cost=seq_cost)
+    segs, _ = oracle.flat_segments(lens, flat, seq_cost=seq_cost)
     ref = oracle.reference_decode(q, c, out_dtype=torch.float32)
     written = set()
     for j, bb, _, _ in segs:
@@ -158,25 +185,28 @@ def test_flat_occupancy_query(kv_dtype, scale_dtype, d):
     assert flat_splits_for(8, 4, 256, n) == flat_splits_for(8, 4, 256, FLAT_WAVES_PER_SIMD)
 
 
-def test_flat_partials_then_merge_equals_decode():
+@pytest.mark.parametrize("seq_cost", [0, 2])
+def test_flat_partials_then_merge_equals_decode(seq_cost):
     """pa_decode_partials + pa_flat_merge is pa_decode, bit for bit."""
     from pagedattn.hip_decode import flat_merge
 
     q, c = _case(LLAMA3_8B, RAGGED, seed=9)
     flat = 29
     b, hq, d = q.shape
-    want = paged_decode_hip(q, c, flat_splits=flat).clone()
+    want = paged_decode_hip(q, c, flat_splits=flat, flat_seq_cost=seq_cost).clone()
     part = torch.empty((b + flat, hq, d), dtype=torch.float32, device="cuda")
     lse = torch.empty((b + flat, hq), dtype=torch.float32, device="cuda")
     out = torch.full_like(q, 3.0)
-    decode_partials(q, c, 1, part_out=part, part_lse=lse, flat_splits=flat, out=out)
-    flat_merge(q, c, flat, part, lse, out)
+    decode_partials(q, c, 1, part_out=part, part_lse=lse, flat_splits=flat, out=out,
+                    flat_seq_cost=seq_cost)
+    flat_merge(q, c, flat, part, lse, out, flat_seq_cost=seq_cost)
     torch.cuda.synchronize()
     assert torch.equal(out, want)
 
 
-@pytest.mark.parametrize("batch,flat", [(130, 37), (300, 256)])
-def test_flat_batches_above_one_wave(batch, flat):
+@pytest.mark.parametrize("batch,flat,seq_cost", [(130, 37, 0), (300, 256, 0), (130, 37, 1), (300, 256, 2),
+                                                 (700, 64, 1)])
+def test_flat_batches_above_one_wave(batch, flat, seq_cost):
     """Batches above 64 sequences: the range locate and the merge scan
     seq_lens in several 64-lane chunks (and the locate takes its second pass)."""
     g = torch.Generator().manual_seed(batch)
@@ -186,7 +216,7 @@ def test_flat_batches_above_one_wave(batch, flat):
     lens[-1] = 0
     shape = ModelShape(8, 2, 64, "b")
     q, c = _case(shape, lens, seed=10)
-    _check(q, c, flat)
+    _check(q, c, flat, seq_cost=seq_cost)
 
 
 def test_flat_sm_scale_override():

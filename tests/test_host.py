@@ -83,7 +83,7 @@ def test_constants_match_header():
     for name in ("PA_ABI_VERSION", "PA_OK", "PA_ERR_INVALID", "PA_ERR_UNSUPPORTED", "PA_ERR_HIP",
                  "PA_KV_FP16", "PA_KV_FP8_E5M2", "PA_KV_INT8", "PA_SCALE_NONE", "PA_SCALE_FP16",
                  "PA_SCALE_FP32", "PA_IO_FP16", "PA_MAX_SPLITS", "PA_MAX_GROUP", "PA_KV_BF16",
-                 "PA_IO_BF16", "PA_MAX_FLAT_SPLITS"):
+                 "PA_IO_BF16", "PA_MAX_FLAT_SPLITS", "PA_MAX_FLAT_SEQ_COST"):
         m = re.search(rf"#define {name} \(?(-?\d+)\)?", text)
         assert m, name
         assert int(m.group(1)) == getattr(_abi, name), name
@@ -126,6 +126,8 @@ INVALID = [
     ("page8", dict(block_size=8), _abi.PA_ERR_UNSUPPORTED),
     ("splits0", dict(num_splits=0), _abi.PA_ERR_INVALID),
     ("splits_big", dict(num_splits=_abi.PA_MAX_SPLITS + 1), _abi.PA_ERR_INVALID),
+    ("seq_cost_neg", dict(flat_seq_cost=-1), _abi.PA_ERR_INVALID),
+    ("seq_cost_big", dict(flat_seq_cost=_abi.PA_MAX_FLAT_SEQ_COST + 1), _abi.PA_ERR_INVALID),
     ("no_workspace", dict(num_splits=4), _abi.PA_ERR_INVALID),
     ("kv_dtype", dict(kv_dtype=7), _abi.PA_ERR_INVALID),
     ("io_dtype", dict(io_dtype=3), _abi.PA_ERR_UNSUPPORTED),

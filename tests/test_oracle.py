@@ -298,6 +298,83 @@ def test_flat_segments_known_answer():
     assert oracle.flat_segments([0, 0], 4) == ([], 1)
 
 
+def test_flat_segments_seq_cost_known_answer():
+    # tiles [4, 2, 4]; cost 2: weights [6, 4, 6], W = 16, per = 8. Sequence 0's
+    # tiles sit at weights 2..5 (range 0), sequence 1's at 8, 9 and sequence
+    # 2's at 12..15 (range 1). Without the charge (per = 5) range 0 also takes
+    # sequence 1's first tile.
+    segs, per = oracle.flat_segments([100, 33, 100], 2, seq_cost=2)
+    assert per == 8 and segs == [(0, 0, 0, 100), (1, 1, 0, 33), (1, 2, 0, 100)]
+    assert oracle.flat_segments([100, 33, 100], 2)[0] == [
+        (0, 0, 0, 100), (0, 1, 0, 32), (1, 1, 32, 33), (1, 2, 0, 100)]
+    # ranges that cover charges only hold no tiles: weights [4, 4], per = 1
+    assert oracle.flat_segments([32, 32], 8, seq_cost=3) == ([(3, 0, 0, 32), (7, 1, 0, 32)], 1)
+    # an empty sequence carries no charge: weights [5, 0, 3], per = 4
+    assert oracle.flat_segments([100, 0, 33], 2, seq_cost=1) == (
+        [(0, 0, 0, 96), (1, 0, 96, 100), (1, 2, 0, 33)], 4)
+
+
+def _flat_segments_brute(seq_lens, flat_splits, seq_cost, align=32):
+    """The weighted flat split by expansion: each non-empty sequence becomes
+    `seq_cost` charge units then one unit per tile, the units are cut into
+    ranges of per = ceil(units / F), and each tile goes to its unit's range."""
+    units = []  # (b, tile index) or None for a charge
+    for b, t in enumerate(seq_lens):
+        n = -(-max(0, t) // align)
+        if n:
+            units += [None] * seq_cost + [(b, k) for k in range(n)]
+    per = max(1, -(-len(units) // flat_splits))
+    pieces = {}
+    for i, u in enumerate(units):
+        if u is not None:
+            pieces.setdefault((i // per, u[0]), []).append(u[1])
+    segs = [(j, b, ks[0] * align, min((ks[-1] + 1) * align, seq_lens[b]))
+            for (j, b), ks in sorted(pieces.items(), key=lambda kv: (kv[0][1], kv[0][0]))]
+    return segs, per
+
+
+@pytest.mark.parametrize("seq_cost", [1, 2, 5])
+@pytest.mark.parametrize("flat_splits", [1, 2, 5, 13, 64, 500])
+def test_flat_segments_seq_cost_against_brute_force(flat_splits, seq_cost):
+    """The closed form (tile k of b at weight cw_b + cost + k) against the
+    expansion into units, and the partition contract."""
+    lens = _ragged_lens()
+    segs, per = oracle.flat_segments(lens, flat_splits, seq_cost=seq_cost)
+    assert (segs, per) == _flat_segments_brute(lens, flat_splits, seq_cost)
+    assert _flat_partition_errors(lens, flat_splits, segs, per) == []
+
+
+@pytest.mark.parametrize("mistake", ["charge_after_tiles", "charge_empty", "charge_per_tile"])
+def test_planted_seq_cost_mistakes_are_caught(mistake):
+    """Mutated weighted work lists disagree with the brute-force expansion."""
+    lens = _ragged_lens()
+    flat_splits, cost = 13, 2
+
+    def mutated(seq_lens, f, c, align=32):
+        tiles = [-(-max(0, t) // align) for t in seq_lens]
+        if mistake == "charge_empty":
+            weights = [n + c for n in tiles]
+        elif mistake == "charge_per_tile":
+            weights = [n * (1 + c) if n else 0 for n in tiles]
+        else:
+            weights = [n + c if n else 0 for n in tiles]
+        per = max(1, -(-sum(weights) // f))
+        segs, cw = [], 0
+        for b, (t, n) in enumerate(zip(seq_lens, tiles)):
+            first = cw if mistake == "charge_after_tiles" else cw + c
+            step = 1 + c if mistake == "charge_per_tile" else 1
+            pieces = {}
+            for k in range(n):
+                pieces.setdefault((first + k * step) // per, []).append(k)
+            for j, ks in sorted(pieces.items()):
+                segs.append((j, b, ks[0] * align, min((ks[-1] + 1) * align, t)))
+            cw += weights[b]
+        return segs, per
+
+    assert mutated(lens, flat_splits, cost) != _flat_segments_brute(lens, flat_splits, cost), \
+        f"{mistake} not caught"
+
+
 def _flat_partition_errors(lens, flat_splits, segs, per):
     """Violations of the flat split's contract by a work list (empty if none)."""
     errs = []
@@ -372,14 +449,14 @@ def test_planted_flat_mistakes_are_caught(mistake):
     assert _flat_partition_errors(lens, flat_splits, segs, per), f"{mistake} not caught"
 
 
-@pytest.mark.parametrize("flat_splits", [1, 3, 8, 40])
-def test_flat_partials_merge_to_reference(flat_splits):
+@pytest.mark.parametrize("flat_splits,seq_cost", [(1, 0), (3, 0), (8, 0), (40, 0), (3, 1), (8, 2)])
+def test_flat_partials_merge_to_reference(flat_splits, seq_cost):
     lens = [1, 33, 500, 0, 96, 260]
     c = _cache(LLAMA3_8B, lens, seed=15)
     q = _q(6, 32, 128, 15)
-    part, lse, whole = oracle.flat_partials(q, c, flat_splits)
+    part, lse, whole = oracle.flat_partials(q, c, flat_splits, seq_cost=seq_cost)
     ref = c_oracle.decode(q, c)
-    segs, _ = oracle.flat_segments(lens, flat_splits)
+    segs, _ = oracle.flat_segments(lens, flat_splits, seq_cost=seq_cost)
     for b, t in enumerate(lens):
         js = [j for j, bb, _, _ in segs if bb == b]
         assert whole[b] == (len(js) == 1)
@@ -636,10 +713,10 @@ def test_flat_needs_merge_agrees_with_the_oracle_work_list():
 
     from pagedattn import flat_needs_merge
 
-    def oracle_needs(lens, flat, max_tokens=None):
+    def oracle_needs(lens, flat, max_tokens=None, seq_cost=0):
         if max_tokens is not None:
             lens = [min(t, max_tokens) for t in lens]
-        segs, _ = oracle.flat_segments(lens, flat)
+        segs, _ = oracle.flat_segments(lens, flat, seq_cost=seq_cost)
         count = [0] * len(lens)
         for _, b, _, _ in segs:
             count[b] += 1
@@ -662,3 +739,6 @@ def test_flat_needs_merge_agrees_with_the_oracle_work_list():
         assert flat_needs_merge(lens, flat) == oracle_needs(lens, flat), (lens, flat)
         cap = rng.choice([32, 64, 512])
         assert flat_needs_merge(lens, flat, cap) == oracle_needs(lens, flat, cap), (lens, flat, cap)
+        cost = rng.randint(1, 4)
+        assert flat_needs_merge(lens, flat, cap, cost) == oracle_needs(lens, flat, cap, cost), \
+            (lens, flat, cap, cost)

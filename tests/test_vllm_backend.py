@@ -204,7 +204,8 @@ def test_decode_forward_takes_the_flat_split_for_large_batches(monkeypatch):
                  seq_lens=torch.full((n,), 4096, dtype=torch.int32))
     impl.kv_sharing_target_layer_name = "shared"
     vb.decode_forward(impl, None, q, q, q, _kv(), meta, torch.zeros_like(q), decode=fake_decode)
-    assert calls[-1] == {"flat_splits": flat_splits_for(8, 4, 256, 2)}
+    # a uniform batch: equal tile ranges (no per-sequence charge)
+    assert calls[-1] == {"flat_splits": flat_splits_for(8, 4, 256, 2), "flat_seq_cost": 0}
     # a small step stays on the classic split
     meta = _meta(max_seq_len=300)
     vb.decode_forward(impl, None, q, q, q, _kv(), meta, torch.zeros_like(q), decode=fake_decode)
@@ -243,7 +244,7 @@ def test_decode_forward_runs_large_short_batches_unsplit(monkeypatch, dtype, lim
                      seq_lens=torch.full((n,), msl, dtype=torch.int32))
         vb.decode_forward(impl, None, q, q, q, _kv(dtype), meta, torch.zeros_like(q), decode=fake_decode)
         if want_flat:
-            assert calls[-1] == {"flat_splits": flat_splits_for(8, 4, 256, 1)}
+            assert calls[-1] == {"flat_splits": flat_splits_for(8, 4, 256, 1), "flat_seq_cost": 0}
         else:
             assert calls[-1] == {"num_splits": 1, "max_seq_len": msl}
     # half the batch (4 workgroups per CU) keeps the flat split
@@ -252,7 +253,7 @@ def test_decode_forward_runs_large_short_batches_unsplit(monkeypatch, dtype, lim
                  seq_lens=torch.full((n // 2,), limit, dtype=torch.int32))
     vb.decode_forward(impl, None, q[: n // 2], q[: n // 2], q[: n // 2], _kv(dtype), meta,
                       torch.zeros_like(q[: n // 2]), decode=fake_decode)
-    assert calls[-1] == {"flat_splits": flat_splits_for(8, 4, 256, 1)}
+    assert calls[-1] == {"flat_splits": flat_splits_for(8, 4, 256, 1), "flat_seq_cost": 0}
 
 
 def _boundary_plan(monkeypatch, lens, msl=None, host_lens=True, kv=torch.float16, shape=(32, 8, 128)):
@@ -281,8 +282,8 @@ def _boundary_plan(monkeypatch, lens, msl=None, host_lens=True, kv=torch.float16
 def _wrapper_plan(lens, kv="fp16", shape=(32, 8, 128)):
     """The launch `paged_decode_hip(num_splits=None)` plans for the same batch."""
     hq, hkv, d = shape
-    s, m, f = plan_decode(lens, hkv, hq // hkv, 256, 1, kv_dtype=kv, head_dim=d)
-    return {"flat_splits": f} if f else {"num_splits": s, "max_seq_len": m}
+    return plan_launch(len(lens), 0, hkv, hq // hkv, 256, 1, kv_dtype=kv, head_dim=d,
+                       seq_lens=lens).launch_kwargs()
 
 
 UNIFORM = [(b, t) for b in (1, 4, 24, 32, 64, 128, 256, 512, 1024, 1100)
