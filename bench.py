@@ -184,21 +184,26 @@ def settle(step, seconds: float = CLOCK_SETTLE_S) -> None:
     torch.cuda.synchronize()
 
 
-def _algorithmic_bytes(cache) -> int:
+def _algo_bytes(lens, shape, elem: int, scale_bytes: int, block_size: int) -> int:
     """K/V (+ int8 scales) inside the sequences + q + out (fp16) + used
     block-table entries."""
-    import torch
+    n_tok = sum(int(t) for t in lens)
+    kv = 2 * n_tok * shape.num_kv_heads * shape.head_dim * elem
+    kv += 2 * n_tok * shape.num_kv_heads * scale_bytes
+    pages = sum(-(-int(t) // block_size) for t in lens)
+    return kv + 2 * len(lens) * shape.num_q_heads * shape.head_dim * 2 + 4 * pages
 
-    lens = cache.seq_lens.cpu().long()
-    s = cache.shape
-    n_tok = int(lens.sum())
-    elem = cache.k_cache.element_size()
-    kv = 2 * n_tok * s.num_kv_heads * s.head_dim * elem
-    if cache.kv_dtype == "int8":
-        kv += 2 * n_tok * s.num_kv_heads * cache.k_scale.element_size()
-    pages = int(((lens + cache.block_size - 1) // cache.block_size).sum())
-    b = int(lens.numel())
-    return kv + 2 * b * s.num_q_heads * s.head_dim * 2 + 4 * pages
+
+def _algorithmic_bytes(cache) -> int:
+    scale = cache.k_scale.element_size() if cache.kv_dtype == "int8" else 0
+    return _algo_bytes(cache.seq_lens.cpu().tolist(), cache.shape, cache.k_cache.element_size(), scale,
+                       cache.block_size)
+
+
+def _workload_algo_bytes(wl: "Workload") -> int:
+    elem = {"fp16": 2, "bf16": 2, "fp8_e5m2": 1, "int8": 1}[wl.kv_dtype]
+    scale = (4 if wl.scale_fp32 else 2) if wl.kv_dtype == "int8" else 0
+    return _algo_bytes(wl.lens, shape_of(wl.shape_name), elem, scale, 16)
 
 
 def bench_write(args, wl, shape, cache, dev) -> int:
@@ -289,6 +294,174 @@ def traffic_for(cfg: str, kernel_name: str) -> tuple[int | None, str]:
         return None, (f"counters were taken on kernel sources {entry.get('source_hash')}, "
                       f"these are {kernel_source_hash()}")
     return entry.get("hbm_bytes_per_launch"), entry.get("source", "")
+
+
+CALIB_COPY_BYTES = 1 << 30  # the --calib-copy device copy
+
+
+def _counter_rows(path: str, counter: str) -> list[tuple[str, float]]:
+    """(kernel name, value in KiB) per dispatch of a rocprofv3 --pmc CSV."""
+    import csv
+
+    with open(path, newline="") as f:
+        return [(r["Kernel_Name"], float(r["Counter_Value"])) for r in csv.DictReader(f)
+                if r["Counter_Name"] == counter]
+
+
+def record_traffic(cfg: str, fetch_csv: str, write_csv: str) -> int:
+    """Turn two rocprofv3 counter runs of `bench.py --config cfg --calib-copy`
+    (one with --pmc FETCH_SIZE, one with --pmc WRITE_SIZE) into HBM bytes per
+    decode launch: each counter's mean over the decode kernel's dispatches,
+    scaled by what the same counter reads for the 1 GiB calibration copy
+    (the largest __amd_rocclr_copyBuffer dispatches). Writes the entry of
+    profiles/traffic.json, keyed to the current kernel sources, and the
+    summary profiles/paged_decode_<cfg>_hbm_counters.md. Runs on the CPU."""
+    import statistics
+
+    wl = make_workload(cfg)
+    algo = _workload_algo_bytes(wl)
+    kib = CALIB_COPY_BYTES / 1024
+    out = {}
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        rows = _counter_rows(path, counter)
+        copies = [v for n, v in rows if "copyBuffer" in n]
+        big = [v for v in copies if v > 0.25 * kib] if counter == "FETCH_SIZE" else \
+              [v for v in copies if v > 0.5 * kib]
+        if not big:
+            raise SystemExit(f"{path}: no calibration copy (run bench.py with --calib-copy)")
+        factor = kib / statistics.median(big)
+        per = {}
+        for name, v in rows:
+            for k in ("paged_decode_flat_kernel", "paged_decode_kernel", "split_reduce_kernel"):
+                if k + "<" in name:
+                    per.setdefault(k, []).append(v)
+        out[counter] = (factor, {k: (statistics.fmean(v), len(v)) for k, v in per.items()},
+                        statistics.median(big))
+    (ff, fetch, fcal), (wf, write, wcal) = out["FETCH_SIZE"], out["WRITE_SIZE"]
+    kernel = "paged_decode_flat_kernel" if "paged_decode_flat_kernel" in fetch else "paged_decode_kernel"
+    if kernel not in fetch or kernel not in write:
+        raise SystemExit(f"no {kernel} dispatches in the counter files")
+    hbm = {k: fetch[k][0] * 1024 * ff + write[k][0] * 1024 * wf for k in fetch if k in write}
+    tfile = ROOT / "profiles" / "traffic.json"
+    data = json.loads(tfile.read_text()) if tfile.exists() else {}
+    summary = f"profiles/paged_decode_{cfg}_hbm_counters.md"
+    data[cfg] = {"kernel": kernel, "hbm_bytes_per_launch": round(hbm[kernel]),
+                 "fetch_factor": round(ff, 4), "write_factor": round(wf, 4),
+                 "source_hash": kernel_source_hash(), "source": summary}
+    tfile.write_text(json.dumps(data, indent=1, sort_keys=True) + "\n")
+    lines = [
+        f"# rocprofv3 HBM counters — paged decode, {cfg}",
+        "",
+        f"Workload: {wl.name}: {wl.description}. Kernel sources: `{kernel_source_hash()}` "
+        "(sha256 prefix of csrc/*.hip, *.h, as `bench.py` computes it).",
+        "",
+        "Commands (two runs; FETCH_SIZE and WRITE_SIZE each in a pass of its own), then the summary",
+        "on the CPU:",
+        "",
+        "```",
+        "cd /root/repo && export TMPDIR=/tmp",
+        f"rocprofv3 --pmc FETCH_SIZE -d gpurun_out/pmc_FETCH_SIZE_{cfg} -o {cfg} --output-format csv -- "
+        f"python3 bench.py --config {cfg} --steps 10 --warmup 2 --no-cpu --calib-copy",
+        f"rocprofv3 --pmc WRITE_SIZE -d gpurun_out/pmc_WRITE_SIZE_{cfg} -o {cfg} --output-format csv -- "
+        f"python3 bench.py --config {cfg} --steps 10 --warmup 2 --no-cpu --calib-copy",
+        f"python3 bench.py --config {cfg} --record-traffic "
+        f"gpurun_out/pmc_FETCH_SIZE_{cfg}/{cfg}_counter_collection.csv "
+        f"gpurun_out/pmc_WRITE_SIZE_{cfg}/{cfg}_counter_collection.csv",
+        "```",
+        "",
+        f"Calibration: the 1 GiB device copy (`__amd_rocclr_copyBuffer`) reads FETCH_SIZE "
+        f"{fcal:,.0f} KiB for {kib:,.0f} KiB read (factor {ff:.4f}) and WRITE_SIZE {wcal:,.0f} KiB "
+        f"for {kib:,.0f} KiB written (factor {wf:.4f}).",
+        "",
+        "| kernel | dispatches | FETCH_SIZE KiB (mean) | WRITE_SIZE KiB (mean) | calibrated HBM bytes / launch |",
+        "|---|---:|---:|---:|---:|",
+    ]
+    for k in sorted(hbm, key=lambda k: -hbm[k]):
+        lines.append(f"| `{k}` | {fetch[k][1]} | {fetch[k][0]:,.1f} | {write[k][0]:,.1f} | {hbm[k]:,.0f} |")
+    lines += ["", f"Algorithmic bytes per decode call: {algo:,}. Calibrated traffic of `{kernel}` / "
+                  f"algorithmic = {hbm[kernel] / algo:.4f}.", ""]
+    (ROOT / summary).write_text("\n".join(lines))
+    _log(f"{cfg}: {kernel} {hbm[kernel]:,.0f} B/launch = {hbm[kernel] / algo:.4f} x algorithmic "
+         f"(fetch x{ff:.3f}, write x{wf:.3f}); wrote {summary}")
+    return 0
+
+
+def record_trace(cfg: str, stats_csv: str, trace_csv: str, bench_out: str) -> int:
+    """Summarise a `rocprofv3 --kernel-trace --stats` run of `bench.py
+    --config cfg` into profiles/paged_decode_<cfg>_kernel_trace.md: the top
+    kernels, the bench line the same run printed, and the decode kernel's
+    rocprof average over the bench's kernel-alone loop (the longest run of
+    decode dispatches with no merge between them, its last --steps ones)
+    beside the bench's HIP-event figure. Runs on the CPU."""
+    import csv
+    import statistics
+
+    wl = make_workload(cfg)
+    line = next(l for l in reversed(pathlib.Path(bench_out).read_text().splitlines()) if l.startswith("{"))
+    bench = json.loads(line)
+    steps = int(bench["steps"])
+    with open(stats_csv, newline="") as f:
+        stats = list(csv.DictReader(f))
+    with open(trace_csv, newline="") as f:
+        trace = [(int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]) for r in csv.DictReader(f)]
+    trace.sort()
+    kernel = bench["roofline"]["kernel"]
+    runs, cur = [], []
+    for t0, t1, name in trace:
+        if kernel + "<" in name:
+            cur.append((t1 - t0) / 1e3)
+        elif "split_reduce_kernel" in name or "paged_decode" in name:
+            if cur:
+                runs.append(cur)
+            cur = []
+    if cur:
+        runs.append(cur)
+    alone = max(runs, key=len)[-steps:]
+    short = lambda n: n.replace("(anonymous namespace)::", "").split("(")[0].replace("void ", "")[:90]
+    cmd = (f"cd /root/repo && export TMPDIR=/tmp && rocprofv3 --kernel-trace --stats -d gpurun_out/trace_{cfg} "
+           f"-o {cfg} --output-format csv -- python3 bench.py --config {cfg} --steps {steps} "
+           f"--warmup {bench['warmup']} --no-cpu")
+    lines = [
+        f"# rocprofv3 kernel trace — paged decode, {cfg} ({wl.name}: {wl.description})",
+        "",
+        f"Kernel sources: `{kernel_source_hash()}`. Command (from the repo root, on one MI355X), then",
+        "the summary on the CPU:",
+        "",
+        "```",
+        cmd + f" > gpurun_out/trace_{cfg}.out",
+        f"python3 bench.py --config {cfg} --record-trace gpurun_out/trace_{cfg}/{cfg}_kernel_stats.csv "
+        f"gpurun_out/trace_{cfg}/{cfg}_kernel_trace.csv gpurun_out/trace_{cfg}.out",
+        "```",
+        "",
+        f"Kernel stats (`{cfg}_kernel_stats.csv`, top entries; durations in µs):",
+        "",
+        "| kernel | calls | avg µs | min µs | max µs | % time |",
+        "|---|---:|---:|---:|---:|---:|",
+    ]
+    for r in stats[:6]:
+        lines.append(f"| `{short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                     f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | {float(r['Percentage']):.1f} |")
+    avg = statistics.fmean(alone)
+    lines += [
+        "",
+        f"Agreement: the bench's kernel-alone loop (HIP events over {steps} launches) = "
+        f"{bench['roofline']['kernel_us']:.2f} µs; the same {len(alone)} dispatches in rocprof's trace average "
+        f"{avg:.2f} µs (median {statistics.median(alone):.2f})."
+        + (" That eager loop is host-bound at this size (each launch waits for the Python call that "
+           "makes it; more so under the tracer): rocprof's average is the kernel's own time."
+           if bench["roofline"]["kernel_us"] > 1.2 * avg else ""),
+        "",
+        "The bench line printed by the same run:",
+        "",
+        "```",
+        line,
+        "```",
+        "",
+    ]
+    out = ROOT / "profiles" / f"paged_decode_{cfg}_kernel_trace.md"
+    out.write_text("\n".join(lines))
+    _log(f"{cfg}: bench kernel {bench['roofline']['kernel_us']:.2f} us, rocprof {avg:.2f} us; wrote {out.name}")
+    return 0
 
 
 def _graph_us(fn, calls: int, reps: int) -> float:
@@ -535,9 +708,24 @@ def main() -> int:
     ap.add_argument("--write-tokens", type=int, default=65536)
     ap.add_argument("--flat", type=int, default=None,
                     help="flat (work-balanced) split with this many ranges per kv head; 0 = classic")
+    ap.add_argument("--record-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"), default=None,
+                    help="CPU only: fold two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of "
+                         "--config into profiles/traffic.json and its counter summary")
+    ap.add_argument("--record-trace", nargs=3, metavar=("STATS_CSV", "TRACE_CSV", "BENCH_OUT"), default=None,
+                    help="CPU only: summarise a rocprofv3 --kernel-trace --stats run of --config "
+                         "into its profiles/ summary")
     ap.add_argument("--seq-cost", type=int, default=None,
                     help="override the flat split's per-sequence charge in tiles (flat_seq_cost)")
     args = ap.parse_args()
+
+    if args.record_traffic:
+        if not args.config:
+            raise SystemExit("--record-traffic needs --config")
+        return record_traffic(args.config, *args.record_traffic)
+    if args.record_trace:
+        if not args.config:
+            raise SystemExit("--record-trace needs --config")
+        return record_trace(args.config, *args.record_trace)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
