@@ -549,8 +549,13 @@ def measure(cfg: str, args, dev, cpu: bool) -> dict:
     # bit stability now; parity of sampled sequences against the CPU oracle
     # after the timed regions, so that seconds of CPU work do not leave the
     # GPU idle (and clocked down) right before them
+    # the workload's lengths are known on the host, as a serving step's are
+    host = None if (args.no_host_lens or not flat) else torch.tensor(wl.lens, dtype=torch.int32)
+    if host is not None:
+        launch += ", host lengths"
     step = lambda i: paged_decode_hip(q, caches[i % copies], out=out, num_splits=splits,
-                                      max_seq_len=msl, flat_splits=flat, flat_seq_cost=cost)
+                                      max_seq_len=msl, flat_splits=flat, flat_seq_cost=cost,
+                                      seq_lens_host=host)
     step(0)
     first = out.clone()
     step(0)
@@ -590,7 +595,7 @@ def measure(cfg: str, args, dev, cpu: bool) -> dict:
     if flat:
         fo, fl = _WS.get_flat(wl.batch + flat, shape.num_q_heads, shape.head_dim, dev)
         run = lambda c: decode_partials(q, c, 1, part_out=fo, part_lse=fl, flat_splits=flat, out=out,
-                                        flat_seq_cost=cost)
+                                        flat_seq_cost=cost, seq_lens_host=host)
     elif splits > 1:
         part_out, part_lse = _WS.get(wl.batch, shape.num_q_heads, splits, shape.head_dim, dev)
         run = lambda c: decode_partials(q, c, splits, part_out=part_out, part_lse=part_lse,
@@ -616,7 +621,7 @@ def measure(cfg: str, args, dev, cpu: bool) -> dict:
     merge = None
     if flat:
         run(caches[0])  # the slots of one pass
-        merge = lambda i: flat_merge(q, caches[0], flat, fo, fl, out, flat_seq_cost=cost)
+        merge = lambda i: flat_merge(q, caches[0], flat, fo, fl, out, flat_seq_cost=cost, seq_lens_host=host)
     elif splits > 1:
         merge = lambda i: split_reduce(part_out, part_lse, out)
     if merge is not None:
@@ -714,6 +719,9 @@ def main() -> int:
     ap.add_argument("--record-trace", nargs=3, metavar=("STATS_CSV", "TRACE_CSV", "BENCH_OUT"), default=None,
                     help="CPU only: summarise a rocprofv3 --kernel-trace --stats run of --config "
                          "into its profiles/ summary")
+    ap.add_argument("--no-host-lens", action="store_true",
+                    help="flat split: let the kernels scan seq_lens on the GPU instead of passing the "
+                         "workload's lengths from the host (seq_lens_host)")
     ap.add_argument("--seq-cost", type=int, default=None,
                     help="override the flat split's per-sequence charge in tiles (flat_seq_cost)")
     args = ap.parse_args()

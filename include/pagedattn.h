@@ -57,7 +57,7 @@
 extern "C" {
 #endif
 
-#define PA_ABI_VERSION 6
+#define PA_ABI_VERSION 7
 
 /* Return codes. */
 #define PA_OK 0
@@ -92,6 +92,8 @@ extern "C" {
 #define PA_MAX_FLAT_SPLITS 65536
 #define PA_MAX_FLAT_SEQ_COST 64
 #define PA_MAX_GROUP 16
+/* Entries of the host-built launch tables (see seq_lens_host). */
+#define PA_HOST_TABLE_MAX 256
 
 typedef struct pa_decode_args {
   /* device pointers */
@@ -152,6 +154,16 @@ typedef struct pa_decode_args {
    * (each start costs a wave about one tile of time) holds fewer tiles;
    * suits ragged batches. pa_flat_merge must be given the same value. */
   int32_t flat_seq_cost;
+  /* Flat split only (also an addition): the lengths in host memory, NULL
+   * when the caller has none. Given, they must equal seq_lens. The library
+   * then computes the ranges and the merge's list of cut and empty
+   * sequences on the host and passes them in the kernel arguments, so no
+   * wave reads seq_lens before its first K/V loads and the merge covers only
+   * the sequences that need it (and is not launched when none do). Launches
+   * beyond PA_HOST_TABLE_MAX ranges or merge entries, a batch above 4096 or
+   * sequences of 2^25 tokens and more use the GPU scan as without them.
+   * Read during the call only. */
+  const int32_t *seq_lens_host;
 } pa_decode_args;
 
 typedef struct pa_reduce_args {
@@ -269,6 +281,18 @@ int pa_flat_waves_per_simd(int kv_dtype, int scale_dtype, int head_dim, int *out
  * counterpart in the reference, whose host wrapper allocates its workspace
  * (pagedattn/triton_decode.py:266-282). */
 int pa_decode_noalloc(const pa_decode_args *args, void *stream);
+
+/* The launch tables pa_decode builds from seq_lens_host for a flat split
+ * (flat_splits > 0, seq_lens_host set; the other fields as for pa_decode),
+ * computed on the host without any HIP call: ranges[3 j .. 3 j + 2] = range
+ * j's first sequence, its first 32-token tile there and its tile count (all
+ * zero for a range without tiles); items[3 i .. 3 i + 2] = the i-th sequence
+ * the merge writes (cut by a range boundary, or empty), its first partial
+ * slot and its slot count (0: empty, zeros), *n_items of them. ranges holds
+ * 3 * flat_splits and items 3 * batch int32s. PA_ERR_UNSUPPORTED when the
+ * launch is beyond the tables (the kernels then scan seq_lens). No
+ * counterpart in the reference; for planners and tests. */
+int pa_flat_host_plan(const pa_decode_args *args, int32_t *ranges, int32_t *items, int32_t *n_items);
 
 /* Message for the last non-zero return on the calling thread ("" if none). */
 const char *pa_last_error(void);

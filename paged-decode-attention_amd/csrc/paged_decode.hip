@@ -64,6 +64,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 
@@ -94,6 +95,10 @@ constexpr int kLoadNT = 2;
 // A flat-split wave with at most this many tiles keeps two tiles in flight:
 // short ranges are latency-bound; longer ones stream faster with one.
 constexpr int kDeepTiles = 16;
+// Entries of the launch tables the host builds from host-side lengths (the
+// flat split's ranges, the merge's sequences); larger launches scan seq_lens
+// on the GPU instead.
+constexpr int kHostTab = PA_HOST_TABLE_MAX;
 
 struct KParams {
   const uint8_t *q;
@@ -1223,9 +1228,24 @@ __device__ __forceinline__ void cursor_next(SeqCursor &cur, const ro_i32 *seq_le
 // to 20% later), and that tail costs more than the second wave brings. The
 // register budget is still that of two waves per SIMD, the budget every
 // instance was tuned under.
+// The flat kernel's arguments: the parameters and, when the host knows the
+// lengths (ntab = F > 0), each range's first tile (sequence b in the bits
+// from kTabTBits up, tile t below), tile count and the length of b, so that
+// no wave scans seq_lens before its first loads.
+constexpr int kTabTBits = 20;
+constexpr uint32_t kTabTMask = (1u << kTabTBits) - 1;
+struct FlatArgs {
+  KParams p;
+  int32_t ntab;
+  uint32_t start[kHostTab];
+  uint32_t ntile[kHostTab];
+  uint32_t len[kHostTab];
+};
+
 template <int KV, int SC, int D>
 __global__ void __launch_bounds__(kFlatWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
-paged_decode_flat_kernel(const KParams p) {
+paged_decode_flat_kernel(const FlatArgs fa) {
+  const KParams &p = fa.p;
   using G = Geo<KV, D>;
   static_assert(G::kTT == kSplitAlign, "flat tiles are the kernel's tiles");
   // the workgroup's waves take 4 neighbouring kv heads of one range, so
@@ -1263,7 +1283,15 @@ paged_decode_flat_kernel(const KParams p) {
   // (one pass over seq_lens when the batch fits one wave)
   SeqCursor cc;
   int n;  // this wave's tiles
-  if (p.flat_cost == 0) {
+  if (fa.ntab > 0) {
+    n = (int)fa.ntile[j];
+    if (n == 0) return;
+    const uint32_t st = fa.start[j];
+    cc.b = (int)(st >> kTabTBits);
+    cc.t = (int)(st & kTabTMask);
+    cc.len = (int)fa.len[j];
+    cc.tiles = (cc.len + kSplitAlign - 1) / kSplitAlign;
+  } else if (p.flat_cost == 0) {
     int len0 = 0;
     const int total = flat_total(ro(p.seq_lens), p.batch, p.max_tokens, lane, len0);
     const int per = max(1, (total + p.flat_splits - 1) / p.flat_splits);
@@ -1394,72 +1422,15 @@ enum { kMergeAll = 0, kMergeAuto = 1, kMergeFlat = 2 };
 // synchronise with each other (each stages its weights in its own LDS row).
 constexpr int kMergeWaves = 1;
 
-template <int D, int KIND>
-__global__ void __launch_bounds__(kMergeWaves * 64) split_reduce_kernel(const RParams p) {
+// Fold S partials of row (b, h) into out: the log2-sum-exps at lse[s *
+// lse_step], the normalised rows at part[s * part_step]; lanes cover the
+// head dim, `sw` is the wave's LDS row for the split weights. S == 0 (an
+// empty sequence) writes zeros.
+template <int D>
+__device__ __forceinline__ void merge_into_out(const RParams &p, const float *lse, const float *part,
+                                               int64_t lse_step, int64_t part_step, int S, int b, int h,
+                                               int lane, float *sw) {
   constexpr int kPer = D / 64 > 0 ? D / 64 : 1;  // head-dim elements per lane
-  __shared__ float sw_all[kMergeWaves][kReduceChunk];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  float *sw = sw_all[wave];
-  // XCD-contiguous order, as the split decode launches use: an XCD merges
-  // a contiguous stretch of (sequence, head) pairs, whose partials that
-  // XCD's ranges wrote (0.3-1.3 us per call at C2, C3 and C5)
-  int wg = blockIdx.x;
-  {
-    const int n = gridDim.x, full = n - n % 8;
-    if (wg < full) wg = (wg % 8) * (full / 8) + wg / 8;
-  }
-  const int bh = wg * kMergeWaves + wave;
-  if (bh >= p.batch * p.num_heads) return;
-  const int b = bh / p.num_heads;
-  const int h = bh % p.num_heads;
-  const float *lse = p.part_lse + (int64_t)b * p.slb + (int64_t)h * p.slh;
-  const float *part = p.part_out + (int64_t)b * p.spb + (int64_t)h * p.sph;
-  int64_t lse_step = 1;   // elements between consecutive partials
-  int64_t part_step = p.sps;
-  int S = p.num_splits;
-  if (KIND == kMergeAuto) {
-    const int seq_len = max(0, min(p.seq_lens[b], p.max_tokens));
-    S = split_range(seq_len, p.num_splits, p.max_seq_len, 0).n;
-    if (S <= 1) return;
-  } else if (KIND == kMergeFlat) {
-    // the decode's ranges: per = ceil(total / F) of weight each, where a
-    // non-empty sequence weighs its tiles plus flat_cost
-    const int nt = seq_tiles(ro(p.seq_lens), b, p.max_tokens);
-    const int cost = p.flat_cost;
-    int total = 0, cu = 0;  // all weight, weight before sequence b
-    if (p.batch <= 64) {  // one chunk
-      const int t = lane < p.batch ? seq_tiles(ro(p.seq_lens), lane, p.max_tokens) : 0;
-      total = wave_sum(seq_weight(t, cost));
-      cu = wave_sum(lane < b ? seq_weight(t, cost) : 0);
-    }
-    for (int base = 0; base < p.batch && p.batch > 64; base += 64 * kLenChunks) {
-      int len[kLenChunks];
-      load_len_chunks(ro(p.seq_lens), p.batch, p.max_tokens, base, lane, len);
-      int t = 0, tb = 0;
-#pragma unroll
-      for (int k = 0; k < kLenChunks; ++k) {
-        const int wk = seq_weight(len_tiles(len[k]), cost);
-        t += wk;
-        tb += base + 64 * k + lane < b ? wk : 0;
-      }
-      total += wave_sum(t);
-      cu += wave_sum(tb);
-    }
-    S = 0;  // empty sequence: the merge below writes zeros
-    if (nt > 0) {
-      const int per = max(1, (total + p.num_splits - 1) / p.num_splits);
-      const int first = cu + cost;  // weight of b's tile 0
-      const int j0 = first / per, j1 = (first + nt - 1) / per;
-      if (j0 == j1) return;
-      S = j1 - j0 + 1;
-      lse = p.part_lse + (int64_t)(b + j0) * p.slb + (int64_t)h * p.slh;
-      part = p.part_out + (int64_t)(b + j0) * p.spb + (int64_t)h * p.sph;
-      lse_step = p.slb;
-      part_step = p.spb;
-    }
-  }
-
   const bool active = lane * kPer < D;
   float acc[kPer];
 #pragma unroll
@@ -1546,6 +1517,109 @@ __global__ void __launch_bounds__(kMergeWaves * 64) split_reduce_kernel(const RP
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) wsum += __shfl_xor(wsum, o);
   write_merged<D>(p, acc, wsum, b, h, lane, active);
+}
+
+template <int D, int KIND>
+__global__ void __launch_bounds__(kMergeWaves * 64) split_reduce_kernel(const RParams p) {
+  __shared__ float sw_all[kMergeWaves][kReduceChunk];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  float *sw = sw_all[wave];
+  // XCD-contiguous order, as the split decode launches use: an XCD merges
+  // a contiguous stretch of (sequence, head) pairs, whose partials that
+  // XCD's ranges wrote (0.3-1.3 us per call at C2, C3 and C5)
+  int wg = blockIdx.x;
+  {
+    const int n = gridDim.x, full = n - n % 8;
+    if (wg < full) wg = (wg % 8) * (full / 8) + wg / 8;
+  }
+  const int bh = wg * kMergeWaves + wave;
+  if (bh >= p.batch * p.num_heads) return;
+  const int b = bh / p.num_heads;
+  const int h = bh % p.num_heads;
+  const float *lse = p.part_lse + (int64_t)b * p.slb + (int64_t)h * p.slh;
+  const float *part = p.part_out + (int64_t)b * p.spb + (int64_t)h * p.sph;
+  int64_t lse_step = 1;   // elements between consecutive partials
+  int64_t part_step = p.sps;
+  int S = p.num_splits;
+  if (KIND == kMergeAuto) {
+    const int seq_len = max(0, min(p.seq_lens[b], p.max_tokens));
+    S = split_range(seq_len, p.num_splits, p.max_seq_len, 0).n;
+    if (S <= 1) return;
+  } else if (KIND == kMergeFlat) {
+    // the decode's ranges: per = ceil(total / F) of weight each, where a
+    // non-empty sequence weighs its tiles plus flat_cost
+    const int nt = seq_tiles(ro(p.seq_lens), b, p.max_tokens);
+    const int cost = p.flat_cost;
+    int total = 0, cu = 0;  // all weight, weight before sequence b
+    if (p.batch <= 64) {  // one chunk
+      const int t = lane < p.batch ? seq_tiles(ro(p.seq_lens), lane, p.max_tokens) : 0;
+      total = wave_sum(seq_weight(t, cost));
+      cu = wave_sum(lane < b ? seq_weight(t, cost) : 0);
+    }
+    for (int base = 0; base < p.batch && p.batch > 64; base += 64 * kLenChunks) {
+      int len[kLenChunks];
+      load_len_chunks(ro(p.seq_lens), p.batch, p.max_tokens, base, lane, len);
+      int t = 0, tb = 0;
+#pragma unroll
+      for (int k = 0; k < kLenChunks; ++k) {
+        const int wk = seq_weight(len_tiles(len[k]), cost);
+        t += wk;
+        tb += base + 64 * k + lane < b ? wk : 0;
+      }
+      total += wave_sum(t);
+      cu += wave_sum(tb);
+    }
+    S = 0;  // empty sequence: the merge below writes zeros
+    if (nt > 0) {
+      const int per = max(1, (total + p.num_splits - 1) / p.num_splits);
+      const int first = cu + cost;  // weight of b's tile 0
+      const int j0 = first / per, j1 = (first + nt - 1) / per;
+      if (j0 == j1) return;
+      S = j1 - j0 + 1;
+      lse = p.part_lse + (int64_t)(b + j0) * p.slb + (int64_t)h * p.slh;
+      part = p.part_out + (int64_t)(b + j0) * p.spb + (int64_t)h * p.sph;
+      lse_step = p.slb;
+      part_step = p.spb;
+    }
+  }
+
+  merge_into_out<D>(p, lse, part, lse_step, part_step, S, b, h, lane, sw);
+}
+
+// The flat split's merge when the host knows the lengths: a table of the
+// sequences that need it (cut by a range boundary, or empty), so no wave
+// reads seq_lens. Item i: b (bits 0..15) and its slot count S (bits 16..31;
+// 0 = empty, zeros), and its first slot b + j0. Waves take (item, head)
+// pairs in XCD-contiguous order.
+struct MergeTable {
+  RParams r;
+  int32_t items;
+  uint32_t item[kHostTab];
+  uint32_t slot[kHostTab];
+};
+
+template <int D>
+__global__ void __launch_bounds__(kMergeWaves * 64) flat_merge_table_kernel(const MergeTable a) {
+  const RParams &p = a.r;
+  __shared__ float sw_all[kMergeWaves][kReduceChunk];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  int wg = blockIdx.x;
+  {
+    const int n = gridDim.x, full = n - n % 8;
+    if (wg < full) wg = (wg % 8) * (full / 8) + wg / 8;
+  }
+  const int w = wg * kMergeWaves + wave;
+  if (w >= a.items * p.num_heads) return;
+  const int it = w / p.num_heads;
+  const int h = w % p.num_heads;
+  const uint32_t e = a.item[it];
+  const int b = (int)(e & 0xffffu), S = (int)(e >> 16);
+  const int64_t slot0 = a.slot[it];
+  merge_into_out<D>(p, p.part_lse + slot0 * p.slb + (int64_t)h * p.slh,
+                    p.part_out + slot0 * p.spb + (int64_t)h * p.sph, p.slb, p.spb, S, b, h, lane,
+                    sw_all[wave]);
 }
 
 // ----------------------------------------------------------------------------
@@ -1719,13 +1793,31 @@ int build_params(const pa_decode_args *a, bool need_partials, KParams *kp) {
 // Launch modes beyond the classic kernel's.
 constexpr int kFlat = 3;
 
+// Launch tables built on the host from host-side lengths (pa_decode_args.
+// seq_lens_host): the flat ranges (FlatArgs) and the merge's sequences
+// (MergeTable), the same ranges the kernels would find by scanning seq_lens.
+struct HostPlan {
+  bool ranges = false;       // fa holds the flat ranges
+  bool merge_table = false;  // mt holds every sequence the merge must write
+  bool needs_merge = true;   // some sequence is cut or empty
+  FlatArgs fa;
+  MergeTable mt;
+};
+
 template <int KV, int SC, int D>
-hipError_t launch_decode_t(const KParams &k, int grid, int mode, hipStream_t st) {
+hipError_t launch_decode_t(const KParams &k, int grid, int mode, hipStream_t st, const HostPlan *hp) {
   const dim3 g(grid), blk(kWaves * 64);
   if (mode == kFlat) {
     constexpr int W = kFlatWaves;
     const int flat_grid = (k.hkv * k.head_tiles * k.flat_splits + W - 1) / W;
-    hipLaunchKernelGGL((paged_decode_flat_kernel<KV, SC, D>), dim3(flat_grid), dim3(W * 64), 0, st, k);
+    if (hp != nullptr && hp->ranges) {
+      hipLaunchKernelGGL((paged_decode_flat_kernel<KV, SC, D>), dim3(flat_grid), dim3(W * 64), 0, st, hp->fa);
+    } else {
+      FlatArgs fa;
+      fa.p = k;
+      fa.ntab = 0;
+      hipLaunchKernelGGL((paged_decode_flat_kernel<KV, SC, D>), dim3(flat_grid), dim3(W * 64), 0, st, fa);
+    }
   } else if (mode == kAuto) {
     hipLaunchKernelGGL((paged_decode_kernel<KV, SC, D, kAuto>), g, blk, 0, st, k);
   } else if (mode == kPartials) {
@@ -1737,25 +1829,26 @@ hipError_t launch_decode_t(const KParams &k, int grid, int mode, hipStream_t st)
 }
 
 template <int KV, int SC>
-hipError_t launch_decode_d(const KParams &k, int d, int grid, int mode, hipStream_t st) {
+hipError_t launch_decode_d(const KParams &k, int d, int grid, int mode, hipStream_t st, const HostPlan *hp) {
   switch (d) {
-    case 32: return launch_decode_t<KV, SC, 32>(k, grid, mode, st);
-    case 64: return launch_decode_t<KV, SC, 64>(k, grid, mode, st);
-    case 128: return launch_decode_t<KV, SC, 128>(k, grid, mode, st);
-    default: return launch_decode_t<KV, SC, 256>(k, grid, mode, st);
+    case 32: return launch_decode_t<KV, SC, 32>(k, grid, mode, st, hp);
+    case 64: return launch_decode_t<KV, SC, 64>(k, grid, mode, st, hp);
+    case 128: return launch_decode_t<KV, SC, 128>(k, grid, mode, st, hp);
+    default: return launch_decode_t<KV, SC, 256>(k, grid, mode, st, hp);
   }
 }
 
-hipError_t launch_decode(const KParams &k, const pa_decode_args *a, int mode, hipStream_t st) {
+hipError_t launch_decode(const KParams &k, const pa_decode_args *a, int mode, hipStream_t st,
+                         const HostPlan *hp = nullptr) {
   // the flat launch sizes its own grid from its workgroup width
   const int grid = mode == kFlat ? 0 : a->batch * a->num_kv_heads * k.head_tiles * a->num_splits;
   const int d = a->head_dim;
-  if (a->kv_dtype == PA_KV_FP16) return launch_decode_d<PA_KV_FP16, PA_SCALE_NONE>(k, d, grid, mode, st);
-  if (a->kv_dtype == PA_KV_BF16) return launch_decode_d<PA_KV_BF16, PA_SCALE_NONE>(k, d, grid, mode, st);
+  if (a->kv_dtype == PA_KV_FP16) return launch_decode_d<PA_KV_FP16, PA_SCALE_NONE>(k, d, grid, mode, st, hp);
+  if (a->kv_dtype == PA_KV_BF16) return launch_decode_d<PA_KV_BF16, PA_SCALE_NONE>(k, d, grid, mode, st, hp);
   if (a->kv_dtype == PA_KV_FP8_E5M2)
-    return launch_decode_d<PA_KV_FP8_E5M2, PA_SCALE_NONE>(k, d, grid, mode, st);
-  if (a->scale_dtype == PA_SCALE_FP32) return launch_decode_d<PA_KV_INT8, PA_SCALE_FP32>(k, d, grid, mode, st);
-  return launch_decode_d<PA_KV_INT8, PA_SCALE_FP16>(k, d, grid, mode, st);
+    return launch_decode_d<PA_KV_FP8_E5M2, PA_SCALE_NONE>(k, d, grid, mode, st, hp);
+  if (a->scale_dtype == PA_SCALE_FP32) return launch_decode_d<PA_KV_INT8, PA_SCALE_FP32>(k, d, grid, mode, st, hp);
+  return launch_decode_d<PA_KV_INT8, PA_SCALE_FP16>(k, d, grid, mode, st, hp);
 }
 
 int check_reduce(const pa_reduce_args *r, RParams *rp) {
@@ -1806,6 +1899,85 @@ hipError_t launch_reduce(const RParams &rp, int batch, int d, hipStream_t st) {
     default: hipLaunchKernelGGL((split_reduce_kernel<256, KIND>), dim3(grid), blk, 0, st, rp); break;
   }
   return hipGetLastError();
+}
+
+hipError_t launch_merge_table(const MergeTable &mt, int d, hipStream_t st) {
+  const int grid = (mt.items * mt.r.num_heads + kMergeWaves - 1) / kMergeWaves;
+  const dim3 blk(kMergeWaves * 64);
+  switch (d) {
+    case 32: hipLaunchKernelGGL((flat_merge_table_kernel<32>), dim3(grid), blk, 0, st, mt); break;
+    case 64: hipLaunchKernelGGL((flat_merge_table_kernel<64>), dim3(grid), blk, 0, st, mt); break;
+    case 128: hipLaunchKernelGGL((flat_merge_table_kernel<128>), dim3(grid), blk, 0, st, mt); break;
+    default: hipLaunchKernelGGL((flat_merge_table_kernel<256>), dim3(grid), blk, 0, st, mt); break;
+  }
+  return hipGetLastError();
+}
+
+// The flat split's ranges and merge list from host-side lengths, exactly as
+// the kernels derive them from seq_lens (flat_locate*, kMergeFlat): lengths
+// clamped to the block table; sequence b weighs its tiles plus flat_cost when
+// non-empty; per = max(1, ceil(W / F)); range j holds the tiles whose weights
+// lie in [j * per, (j + 1) * per). Tables that do not fit (more than
+// kHostTab ranges or merge entries, a batch over 4096, sequences of 2^20
+// tiles) are left off and the kernels scan seq_lens.
+void build_host_plan(const pa_decode_args *a, const KParams &k, HostPlan *hp) {
+  hp->ranges = hp->merge_table = false;
+  hp->needs_merge = true;
+  if (a->seq_lens_host == nullptr || a->flat_splits <= 0) return;
+  const int F = a->flat_splits, B = a->batch, cost = k.flat_cost;
+  const int64_t max_tiles = ((int64_t)k.max_tokens + kSplitAlign - 1) / kSplitAlign;
+  int64_t W = 0;
+  for (int b = 0; b < B; ++b) {
+    const int t = (std::max(0, std::min(a->seq_lens_host[b], k.max_tokens)) + kSplitAlign - 1) / kSplitAlign;
+    W += t > 0 ? t + cost : 0;
+  }
+  const int64_t per = std::max<int64_t>(1, (W + F - 1) / F);
+  const bool ranges = F <= kHostTab && B <= (1 << (32 - kTabTBits)) && max_tiles <= (int64_t)kTabTMask;
+  FlatArgs &fa = hp->fa;
+  MergeTable &mt = hp->mt;
+  if (ranges) {
+    fa.p = k;
+    fa.ntab = F;
+    for (int j = 0; j < F; ++j) fa.start[j] = fa.ntile[j] = fa.len[j] = 0;
+  }
+  int items = 0;
+  bool fits = B <= 0xffff;
+  int64_t cw = 0;
+  for (int b = 0; b < B; ++b) {
+    const int len = std::max(0, std::min(a->seq_lens_host[b], k.max_tokens));
+    const int t = (len + kSplitAlign - 1) / kSplitAlign;
+    int S = 0;
+    int64_t slot = 0;
+    if (t > 0) {
+      const int64_t first = cw + cost;  // weight of tile 0
+      const int64_t j0 = first / per, j1 = (first + t - 1) / per;
+      if (ranges) {
+        for (int64_t j = j0; j <= j1; ++j) {
+          const int64_t lo = std::max(first, j * per), hi = std::min(first + t, (j + 1) * per);
+          if (fa.ntile[j] == 0) {
+            fa.start[j] = ((uint32_t)b << kTabTBits) | (uint32_t)(lo - first);
+            fa.len[j] = (uint32_t)len;
+          }
+          fa.ntile[j] += (uint32_t)(hi - lo);
+        }
+      }
+      cw += t + cost;
+      if (j0 == j1) continue;  // inside one range: the decode pass writes it
+      S = (int)(j1 - j0 + 1);
+      slot = b + j0;
+    }
+    if (items < kHostTab && fits) {
+      mt.item[items] = (uint32_t)b | ((uint32_t)S << 16);
+      mt.slot[items] = (uint32_t)slot;
+    }
+    ++items;
+  }
+  hp->ranges = ranges;
+  hp->needs_merge = items > 0;
+  if (items <= kHostTab && fits) {
+    hp->merge_table = true;
+    mt.items = items;
+  }
 }
 
 pa_reduce_args reduce_args_from(const pa_decode_args *a) {
@@ -1912,11 +2084,18 @@ int pa_decode(const pa_decode_args *a, void *stream) {
   }
   if (a->batch == 0) return ok();
   hipStream_t st = static_cast<hipStream_t>(stream);
-  hipError_t e = launch_decode(k, a, flat ? kFlat : split ? kAuto : kUnsplit, st);
+  HostPlan plan;
+  if (flat) build_host_plan(a, k, &plan);
+  hipError_t e = launch_decode(k, a, flat ? kFlat : split ? kAuto : kUnsplit, st, &plan);
   if (e != hipSuccess) return fail(PA_ERR_HIP, "decode launch failed: %s", hipGetErrorString(e));
-  if (split) {
-    e = flat ? launch_reduce<kMergeFlat>(rp, a->batch, a->head_dim, st)
-             : launch_reduce<kMergeAuto>(rp, a->batch, a->head_dim, st);
+  if (split && !(flat && !plan.needs_merge)) {
+    if (flat && plan.merge_table) {
+      plan.mt.r = rp;
+      e = launch_merge_table(plan.mt, a->head_dim, st);
+    } else {
+      e = flat ? launch_reduce<kMergeFlat>(rp, a->batch, a->head_dim, st)
+               : launch_reduce<kMergeAuto>(rp, a->batch, a->head_dim, st);
+    }
     if (e != hipSuccess) return fail(PA_ERR_HIP, "reduce launch failed: %s", hipGetErrorString(e));
   }
   return ok();
@@ -1969,8 +2148,10 @@ int pa_decode_partials(const pa_decode_args *a, void *stream) {
   int rc = build_params(a, true, &k);
   if (rc != PA_OK) return rc;
   if (a->batch == 0) return ok();
+  HostPlan plan;
+  if (a->flat_splits > 0) build_host_plan(a, k, &plan);
   hipError_t e = launch_decode(k, a, a->flat_splits > 0 ? kFlat : kPartials,
-                               static_cast<hipStream_t>(stream));
+                               static_cast<hipStream_t>(stream), &plan);
   if (e != hipSuccess) return fail(PA_ERR_HIP, "decode launch failed: %s", hipGetErrorString(e));
   return ok();
 }
@@ -1990,8 +2171,43 @@ int pa_flat_merge(const pa_decode_args *a, void *stream) {
   rp.num_splits = a->flat_splits;
   rp.flat_cost = a->flat_seq_cost;
   if (a->batch == 0) return ok();
-  hipError_t e = launch_reduce<kMergeFlat>(rp, a->batch, a->head_dim, static_cast<hipStream_t>(stream));
+  HostPlan plan;
+  build_host_plan(a, k, &plan);
+  if (!plan.needs_merge) return ok();  // every sequence inside one range: nothing to fold
+  hipError_t e;
+  if (plan.merge_table) {
+    plan.mt.r = rp;
+    e = launch_merge_table(plan.mt, a->head_dim, static_cast<hipStream_t>(stream));
+  } else {
+    e = launch_reduce<kMergeFlat>(rp, a->batch, a->head_dim, static_cast<hipStream_t>(stream));
+  }
   if (e != hipSuccess) return fail(PA_ERR_HIP, "reduce launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int pa_flat_host_plan(const pa_decode_args *a, int32_t *ranges, int32_t *items, int32_t *n_items) {
+  if (ranges == nullptr || items == nullptr || n_items == nullptr)
+    return fail(PA_ERR_INVALID, "ranges, items and n_items must be non-NULL");
+  KParams k;
+  int rc = build_params(a, true, &k);
+  if (rc != PA_OK) return rc;
+  if (a->flat_splits <= 0 || a->seq_lens_host == nullptr)
+    return fail(PA_ERR_INVALID, "pa_flat_host_plan needs flat_splits > 0 and seq_lens_host");
+  HostPlan plan;
+  build_host_plan(a, k, &plan);
+  if (!plan.ranges || !plan.merge_table)
+    return fail(PA_ERR_UNSUPPORTED, "this launch does not fit the host tables (the kernels scan seq_lens)");
+  for (int j = 0; j < a->flat_splits; ++j) {
+    ranges[3 * j] = (int32_t)(plan.fa.start[j] >> kTabTBits);
+    ranges[3 * j + 1] = (int32_t)(plan.fa.start[j] & kTabTMask);
+    ranges[3 * j + 2] = (int32_t)plan.fa.ntile[j];
+  }
+  *n_items = plan.mt.items;
+  for (int i = 0; i < plan.mt.items; ++i) {
+    items[3 * i] = (int32_t)(plan.mt.item[i] & 0xffffu);
+    items[3 * i + 1] = (int32_t)plan.mt.slot[i];
+    items[3 * i + 2] = (int32_t)(plan.mt.item[i] >> 16);
+  }
   return ok();
 }
 

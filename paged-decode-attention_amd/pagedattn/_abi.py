@@ -12,7 +12,7 @@ import os
 import pathlib
 import threading
 
-PA_ABI_VERSION = 6
+PA_ABI_VERSION = 7
 
 PA_OK = 0
 PA_ERR_INVALID = -1
@@ -36,6 +36,7 @@ PA_MAX_FLAT_SPLITS = 65536
 PA_MAX_FLAT_SEQ_COST = 64
 PA_NOALLOC_SCRATCH_BYTES = 32 << 20
 PA_MAX_GROUP = 16
+PA_HOST_TABLE_MAX = 256
 
 LIB_NAME = "libpagedattn_hip.so"
 
@@ -48,6 +49,7 @@ EXPORTED_SYMBOLS = (
     "pa_cache_write",
     "pa_flat_merge",
     "pa_flat_waves_per_simd",
+    "pa_flat_host_plan",
     "pa_last_error",
     "pa_abi_version",
 )
@@ -99,6 +101,7 @@ class PaDecodeArgs(ctypes.Structure):
         ("sm_scale", ctypes.c_float),
         ("flat_splits", _i32),
         ("flat_seq_cost", _i32),
+        ("seq_lens_host", _vp),
     ]
 
 
@@ -195,6 +198,8 @@ def load() -> ctypes.CDLL:
         lib.pa_flat_waves_per_simd.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                                   ctypes.POINTER(ctypes.c_int)]
         lib.pa_flat_waves_per_simd.restype = ctypes.c_int
+        lib.pa_flat_host_plan.argtypes = [ctypes.POINTER(PaDecodeArgs), _vp, _vp, _vp]
+        lib.pa_flat_host_plan.restype = ctypes.c_int
         lib.pa_last_error.argtypes = []
         lib.pa_last_error.restype = ctypes.c_char_p
         lib.pa_abi_version.argtypes = []

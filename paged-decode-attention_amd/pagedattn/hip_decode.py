@@ -529,6 +529,7 @@ def _fill_args(
     max_seq_len: int = 0,
     flat_splits: int = 0,
     flat_seq_cost: int = 0,
+    seq_lens_host: torch.Tensor | None = None,
 ) -> _abi.PaDecodeArgs:
     b, hq, d = q.shape
     shape = cache.shape
@@ -597,6 +598,13 @@ def _fill_args(
             pst = part_out.stride()[:3]
         lst = part_lse.stride()[:2]
 
+    host_ptr = None
+    if seq_lens_host is not None and flat_splits > 0:
+        if (seq_lens_host.device.type != "cpu" or seq_lens_host.dtype != torch.int32
+                or tuple(seq_lens_host.shape) != (b,) or not seq_lens_host.is_contiguous()):
+            raise ValueError(f"seq_lens_host must be a contiguous int32 CPU tensor of shape ({b},)")
+        host_ptr = seq_lens_host.data_ptr()
+
     # one constructor call, fields in declaration order (include/pagedattn.h)
     return _abi.PaDecodeArgs(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), k_scale, v_scale, out.data_ptr(), po, pl,
@@ -606,7 +614,7 @@ def _fill_args(
         qst[0], qst[1], kst[0], kst[1], kst[2], sst[0], sst[1], ost[0], ost[1],
         pst[0], pst[1], pst[2], lst[0], lst[1], btst[0],
         _KV_CODE[kv_dtype], scale_code, _IO_CODE[q.dtype], sm_scale, int(flat_splits),
-        int(flat_seq_cost))
+        int(flat_seq_cost), host_ptr)
 
 
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
@@ -642,6 +650,7 @@ def paged_decode_hip(
     max_seq_len: int | None = None,
     flat_splits: int | None = None,
     flat_seq_cost: int | None = None,
+    seq_lens_host: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Paged GQA decode attention. q: [B, Hq, D] fp16|bf16 -> [B, Hq, D] in q's dtype.
 
@@ -669,6 +678,13 @@ def paged_decode_hip(
     `flat_splits`) charges each sequence that many tiles of weight when the
     ranges are cut, which balances ranges that start several sequences
     (`plan_launch` sets RAGGED_FLAT_SEQ_COST for ragged batches).
+
+    `seq_lens_host` (an addition): the lengths as a contiguous int32 CPU
+    tensor equal to `cache.seq_lens`, when the caller has them (a serving
+    step's metadata usually does). A flat launch then takes its ranges and
+    its merge list from the host (no seq_lens scan on the GPU, no merge
+    launch when no sequence is cut or empty). With `num_splits=None` the
+    lengths come to the host anyway and are used so.
     """
     del per_page_bt, num_warps, num_stages
     b, hq, d = q.shape
@@ -691,6 +707,8 @@ def paged_decode_hip(
     elif num_splits is None:
         # the lengths come to the host in the one sync the reference also makes
         lens = cache.seq_lens.tolist()
+        if seq_lens_host is None:
+            seq_lens_host = torch.tensor(lens, dtype=torch.int32)
         wps = flat_waves_per_simd(cache.kv_dtype, d, None if cache.k_scale is None else cache.k_scale.dtype)
         plan = plan_launch(b, 0, hkv, group, _cu_count(q.device), wps, kv_dtype=cache.kv_dtype,
                            head_dim=d, seq_lens=lens)
@@ -713,7 +731,7 @@ def paged_decode_hip(
     elif num_splits > 1:
         part_out, part_lse = _WS.get(b, hq, num_splits, d, q.device)
     args = _fill_args(q, cache, out, num_splits, scale, part_out, part_lse, max_seq_len or 0, flat,
-                      int(flat_seq_cost or 0) if flat else 0)
+                      int(flat_seq_cost or 0) if flat else 0, seq_lens_host)
     lib = _abi.load()
     if flat > 0 and not merge:
         # every sequence inside one range: the decode pass writes all of out
@@ -739,6 +757,7 @@ def decode_noalloc(
     flat_splits: int = 0,
     sm_scale: float | None = None,
     flat_seq_cost: int = 0,
+    seq_lens_host: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """The decode through pa_decode_noalloc, which allocates nothing.
 
@@ -756,7 +775,7 @@ def decode_noalloc(
     scale = cache.shape.softmax_scale if sm_scale is None else float(sm_scale)
     flat = int(flat_splits or 0)
     args = _fill_args(q, cache, out, 1 if flat else int(num_splits), scale, None, None,
-                      int(max_seq_len or 0), flat, int(flat_seq_cost or 0) if flat else 0)
+                      int(max_seq_len or 0), flat, int(flat_seq_cost or 0) if flat else 0, seq_lens_host)
     lib = _abi.load()
     rc = _call(q.device, lib.pa_decode_noalloc, ctypes.byref(args), _stream(q.device))
     _abi.check(rc, "pa_decode_noalloc")
@@ -774,6 +793,7 @@ def decode_partials(
     flat_splits: int = 0,
     out: torch.Tensor | None = None,
     flat_seq_cost: int = 0,
+    seq_lens_host: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Run only the decode pass; returns (part_out [B,Hq,S,D], part_lse [B,Hq,S]).
 
@@ -782,8 +802,8 @@ def decode_partials(
     of the reference's split epilogue (triton_decode.py:169-188).
     With `flat_splits` = F > 0 it is the flat decode pass: the partials are
     slots [B + F, Hq, D] / [B + F, Hq], and sequences that one wave range
-    holds whole are written to `out`; `flat_seq_cost` as for
-    `paged_decode_hip`.
+    holds whole are written to `out`; `flat_seq_cost` and `seq_lens_host`
+    as for `paged_decode_hip`.
     """
     b, hq, d = q.shape
     scale = cache.shape.softmax_scale if sm_scale is None else float(sm_scale)
@@ -801,7 +821,7 @@ def decode_partials(
         out = torch.empty((b, hq, d), dtype=q.dtype, device=q.device)
     _check_partials(q.device, part_out, part_lse, b, hq, d, num_splits, flat_splits)
     args = _fill_args(q, cache, out, num_splits, scale, part_out, part_lse, max_seq_len, flat_splits,
-                      flat_seq_cost if flat_splits > 0 else 0)
+                      flat_seq_cost if flat_splits > 0 else 0, seq_lens_host)
     lib = _abi.load()
     rc = _call(q.device, lib.pa_decode_partials, ctypes.byref(args), _stream(q.device))
     _abi.check(rc, "pa_decode_partials")
@@ -817,6 +837,7 @@ def flat_merge(
     out: torch.Tensor,
     sm_scale: float | None = None,
     flat_seq_cost: int = 0,
+    seq_lens_host: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """The flat split's merge pass alone: after `decode_partials(...,
     flat_splits=F, out=out, flat_seq_cost=c)` with the same arguments, folds
@@ -827,7 +848,8 @@ def flat_merge(
     scale = cache.shape.softmax_scale if sm_scale is None else float(sm_scale)
     b, hq, d = q.shape
     _check_partials(q.device, part_out, part_lse, b, hq, d, 1, flat_splits)
-    args = _fill_args(q, cache, out, 1, scale, part_out, part_lse, 0, flat_splits, flat_seq_cost)
+    args = _fill_args(q, cache, out, 1, scale, part_out, part_lse, 0, flat_splits, flat_seq_cost,
+                      seq_lens_host)
     lib = _abi.load()
     rc = _call(q.device, lib.pa_flat_merge, ctypes.byref(args), _stream(q.device))
     _abi.check(rc, "pa_flat_merge")
