@@ -72,13 +72,17 @@ FLAT_WAVES_PER_SIMD_KV = {"int8": 2}
 MIN_FLAT_TILES_PER_WAVE = 4
 # Tiles of weight the flat split charges each sequence of a ragged batch
 # (flat_seq_cost): a wave that starts a sequence loads a new q, stores a
-# result and restarts its tile pipeline, about 0.9 us against 1.0 us per fp8
-# tile at head_dim 128 (per-wave timestamps, Llama-3-8B shape, C3's lengths:
-# ranges of 27 tiles ended 2.7 us later when they held 4 sequences than when
-# they held 1). Nearly uniform batches keep 0: their ranges then fall on
+# result and restarts its tile pipeline, a fixed time, so the charge in
+# tiles grows as the tiles shrink: 1 for 2-byte KV, 2 for 1-byte KV
+# (RAGGED_FLAT_SEQ_COST_KV). Whole calls at the Llama-3-8B shape on C3's
+# lengths (B = 64, T log-uniform 128..8192, F = 128; int8 F = 256), charge
+# 0 / 1 / 2 / 3 tiles: fp8 - / 40.5 / 40.1 / 40.2 us (3 repetitions each,
+# 0: 41.4), int8 + fp32 scales 52.2 / 50.8 / 49.1 / 50.1, fp16 73.5 / 72.7 /
+# 73.0 / 72.8. Nearly uniform batches keep 0: their ranges then fall on
 # sequence boundaries or cut every sequence alike, and a charge would only
 # unbalance them.
 RAGGED_FLAT_SEQ_COST = 1
+RAGGED_FLAT_SEQ_COST_KV = {"fp8_e5m2": 2, "int8": 2}
 # A single sequence up to this many tiles takes the classic split: cut into
 # one chunk per CU it merges 32 partials per head, the flat split 128 (graph-
 # timed whole calls, classic against flat: T = 16384 17.9 / 21.0 us, 32768
@@ -310,7 +314,8 @@ def plan_launch(batch: int, max_seq_len: int, num_kv_heads: int, group: int, sm_
             unless the flat split needs no merge either (`flat_needs_merge`);
       * otherwise the classic split (`plan_num_splits`), on the known
         lengths or on `batch` sequences of `max_seq_len` tokens.
-    A flat plan charges each sequence RAGGED_FLAT_SEQ_COST tiles when the
+    A flat plan charges each sequence RAGGED_FLAT_SEQ_COST tiles
+    (RAGGED_FLAT_SEQ_COST_KV for 1-byte KV) when the
     lengths are known and not nearly uniform, else nothing.
     """
     cus = max(1, sm_count)
@@ -328,7 +333,8 @@ def plan_launch(batch: int, max_seq_len: int, num_kv_heads: int, group: int, sm_
                and not (batch == 1 and _tiles(tmax) <= SINGLE_SEQ_SPLIT_MAX_TILES))
     if flat_ok:
         fills = known and _fills_unsplit(lens, num_kv_heads, group, cus)
-        cost = RAGGED_FLAT_SEQ_COST if known and not _nearly_uniform(lens) else 0
+        cost = RAGGED_FLAT_SEQ_COST_KV.get(kv_dtype, RAGGED_FLAT_SEQ_COST) \
+            if known and not _nearly_uniform(lens) else 0
         merge = flat_needs_merge(lens, flat, seq_cost=cost) if known else True
         if kv_dtype is not None and head_dim is not None:
             if short_batch_runs_unsplit(batch, tmax, num_kv_heads, group, cus, kv_dtype,
@@ -677,7 +683,7 @@ def paged_decode_hip(
     (`flat_splits_for`). `flat_seq_cost` (0 when not given with
     `flat_splits`) charges each sequence that many tiles of weight when the
     ranges are cut, which balances ranges that start several sequences
-    (`plan_launch` sets RAGGED_FLAT_SEQ_COST for ragged batches).
+    (`plan_launch` sets RAGGED_FLAT_SEQ_COST(_KV) for ragged batches).
 
     `seq_lens_host` (an addition): the lengths as a contiguous int32 CPU
     tensor equal to `cache.seq_lens`, when the caller has them (a serving

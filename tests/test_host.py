@@ -570,3 +570,26 @@ def test_workspace_keeps_outgrown_buffers():
     assert ws._retired[dev][0][0].data_ptr() == p0  # the old buffer is kept alive
     d, _ = ws.get(4, 4, 1, 8, dev)                 # within the 2x growth: no new buffer
     assert d.data_ptr() == c.data_ptr() and len(ws._retired[dev]) == 1
+
+
+def test_plan_charges_ragged_sequences_by_kv_width():
+    """A ragged batch with known lengths is charged RAGGED_FLAT_SEQ_COST tiles
+    per sequence for 2-byte KV and RAGGED_FLAT_SEQ_COST_KV for 1-byte KV (a
+    sequence start costs a fixed time, more tiles when tiles are half the
+    bytes); nearly uniform batches and unknown lengths are charged nothing."""
+    import math
+
+    from pagedattn.hip_decode import (RAGGED_FLAT_SEQ_COST, RAGGED_FLAT_SEQ_COST_KV, plan_launch)
+
+    g = torch.Generator().manual_seed(2)
+    u = torch.rand(64, generator=g, dtype=torch.float64)
+    ragged = torch.exp(math.log(128) + u * (math.log(8192) - math.log(128))).round().long().tolist()
+    for kv, want in (("fp16", RAGGED_FLAT_SEQ_COST), ("bf16", RAGGED_FLAT_SEQ_COST),
+                     ("fp8_e5m2", RAGGED_FLAT_SEQ_COST_KV["fp8_e5m2"]), ("int8", RAGGED_FLAT_SEQ_COST_KV["int8"])):
+        p = plan_launch(64, 0, 8, 4, 256, 2, kv_dtype=kv, head_dim=128, seq_lens=ragged)
+        assert p.flat_splits > 0 and p.flat_seq_cost == want, (kv, p)
+    assert RAGGED_FLAT_SEQ_COST_KV["fp8_e5m2"] == 2 and RAGGED_FLAT_SEQ_COST == 1
+    p = plan_launch(64, 0, 8, 4, 256, 1, kv_dtype="fp8_e5m2", head_dim=128, seq_lens=[4096] * 64)
+    assert p.flat_seq_cost == 0
+    p = plan_launch(64, 8192, 8, 4, 256, 1, kv_dtype="fp8_e5m2", head_dim=128)
+    assert p.flat_seq_cost == 0
