@@ -332,7 +332,8 @@ def record_traffic(cfg: str, fetch_csv: str, write_csv: str) -> int:
         factor = kib / statistics.median(big)
         per = {}
         for name, v in rows:
-            for k in ("paged_decode_flat_kernel", "paged_decode_kernel", "split_reduce_kernel"):
+            for k in ("paged_decode_flat_kernel", "paged_decode_kernel", "split_reduce_kernel",
+                      "flat_merge_table_kernel"):
                 if k + "<" in name:
                     per.setdefault(k, []).append(v)
         out[counter] = (factor, {k: (statistics.fmean(v), len(v)) for k, v in per.items()},
@@ -410,7 +411,7 @@ def record_trace(cfg: str, stats_csv: str, trace_csv: str, bench_out: str) -> in
     for t0, t1, name in trace:
         if kernel + "<" in name:
             cur.append((t1 - t0) / 1e3)
-        elif "split_reduce_kernel" in name or "paged_decode" in name:
+        elif "split_reduce_kernel" in name or "merge_table_kernel" in name or "paged_decode" in name:
             if cur:
                 runs.append(cur)
             cur = []
@@ -461,6 +462,70 @@ def record_trace(cfg: str, stats_csv: str, trace_csv: str, bench_out: str) -> in
     out = ROOT / "profiles" / f"paged_decode_{cfg}_kernel_trace.md"
     out.write_text("\n".join(lines))
     _log(f"{cfg}: bench kernel {bench['roofline']['kernel_us']:.2f} us, rocprof {avg:.2f} us; wrote {out.name}")
+    return 0
+
+
+SQ_COUNTERS = ("SQ_WAVES", "SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_VMEM_RD", "SQ_INSTS_LDS",
+               "SQ_WAVE_CYCLES", "SQ_BUSY_CYCLES", "SQ_WAIT_INST_ANY")
+
+
+def record_sq(paths: list[str]) -> int:
+    """Summarise rocprofv3 --pmc runs of the SQ_COUNTERS (one pass of eight,
+    `bench.py --config cN`, files named `cN_counter_collection.csv`) into
+    profiles/paged_decode_sq_instruction_counts.md: instructions per 32-token
+    tile of one kv head for the flat decode kernel. Tiles per launch come
+    from the workload (sum of ceil(T / 32) over the batch, times kv heads and
+    head tiles). Runs on the CPU."""
+    import csv
+    import statistics
+
+    rows_out = []
+    for path in paths:
+        cfg = pathlib.Path(path).name.split("_")[0]
+        wl = make_workload(cfg)
+        shape = shape_of(wl.shape_name)
+        units = shape.num_kv_heads * -(-shape.gqa_group // 16)
+        tiles = units * sum(-(-t // 32) for t in wl.lens)
+        per = {}
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                if "paged_decode_flat_kernel<" in r["Kernel_Name"]:
+                    per.setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+        if not per:
+            raise SystemExit(f"{path}: no paged_decode_flat_kernel dispatches")
+        m = {k: statistics.median(v) for k, v in per.items()}
+        rows_out.append((cfg, wl, tiles, m))
+    lines = [
+        "# rocprofv3 SQ instruction counters — flat decode kernel",
+        "",
+        f"Kernel sources: `{kernel_source_hash()}`. Commands (from the repo root, on one MI355X; one pass",
+        "of eight SQ counters per config), then the summary on the CPU:",
+        "",
+        "```",
+        "cd /root/repo && export TMPDIR=/tmp",
+        f"rocprofv3 --pmc {' '.join(SQ_COUNTERS)} -d gpurun_out/sq_cN -o cN --output-format csv -- "
+        "python3 bench.py --config cN --steps 10 --warmup 2 --no-cpu",
+        "python3 bench.py --record-sq " + " ".join(f"gpurun_out/sq_{c}/{c}_counter_collection.csv"
+                                                  for c, _, _, _ in rows_out),
+        "```",
+        "",
+        "Each counter is summed over the dispatch's dimensions, the median taken over the",
+        "`paged_decode_flat_kernel` dispatches and divided by the tiles one launch computes (32",
+        "tokens of one kv head each; MFMAs per tile: 8 for Q K^T and 8 for P V at head_dim 128).",
+        "",
+        "| config | waves | tiles / launch | VALU / tile | SALU / tile | LDS / tile | VMEM rd / tile | "
+        "busy / wave cycles |",
+        "|---|---:|---:|---:|---:|---:|---:|---:|",
+    ]
+    for cfg, wl, tiles, m in rows_out:
+        g = lambda k: m.get(k, float("nan"))
+        lines.append(f"| {cfg} ({wl.kv_dtype}) | {g('SQ_WAVES'):,.0f} | {tiles:,} | {g('SQ_INSTS_VALU') / tiles:.0f} | "
+                     f"{g('SQ_INSTS_SALU') / tiles:.0f} | {g('SQ_INSTS_LDS') / tiles:.1f} | "
+                     f"{g('SQ_INSTS_VMEM_RD') / tiles:.1f} | {g('SQ_BUSY_CYCLES'):,.0f} / {g('SQ_WAVE_CYCLES'):,.0f} |")
+    lines.append("")
+    out = ROOT / "profiles" / "paged_decode_sq_instruction_counts.md"
+    out.write_text("\n".join(lines))
+    _log(f"wrote {out.name}")
     return 0
 
 
@@ -722,6 +787,9 @@ def main() -> int:
     ap.add_argument("--no-host-lens", action="store_true",
                     help="flat split: let the kernels scan seq_lens on the GPU instead of passing the "
                          "workload's lengths from the host (seq_lens_host)")
+    ap.add_argument("--record-sq", nargs="+", metavar="CSV", default=None,
+                    help="CPU only: summarise rocprofv3 SQ counter runs (cN_counter_collection.csv) "
+                         "into profiles/paged_decode_sq_instruction_counts.md")
     ap.add_argument("--seq-cost", type=int, default=None,
                     help="override the flat split's per-sequence charge in tiles (flat_seq_cost)")
     args = ap.parse_args()
@@ -730,6 +798,8 @@ def main() -> int:
         if not args.config:
             raise SystemExit("--record-traffic needs --config")
         return record_traffic(args.config, *args.record_traffic)
+    if args.record_sq:
+        return record_sq(args.record_sq)
     if args.record_trace:
         if not args.config:
             raise SystemExit("--record-trace needs --config")
