@@ -177,12 +177,17 @@ def decode_forward(impl, layer, query, key, value, kv_cache, attn_metadata, outp
     # lengths on the host (`seq_lens_cpu`) gives the planner the whole batch,
     # the same input `paged_decode_hip(num_splits=None)` plans from;
     # otherwise it plans for a ragged batch of up to max_seq_len tokens.
+    # A flat launch planned on host lengths also takes them (its ranges and
+    # merge list are then built on the host).
     msl = int(attn_metadata.max_seq_len)
+    host = _host_seq_lens(attn_metadata, n)
     plan = plan_launch(n, msl, impl.num_kv_heads, impl.num_heads // impl.num_kv_heads,
                        _cu_count(query.device), flat_waves_per_simd(cache.kv_dtype, impl.head_size),
-                       kv_dtype=cache.kv_dtype, head_dim=impl.head_size,
-                       seq_lens=_host_seq_lens(attn_metadata, n))
-    decode(query[:n], cache, out=output[:n], sm_scale=impl.scale, **plan.launch_kwargs())
+                       kv_dtype=cache.kv_dtype, head_dim=impl.head_size, seq_lens=host)
+    kw = plan.launch_kwargs()
+    if plan.flat_splits and host is not None:
+        kw["seq_lens_host"] = torch.tensor(host, dtype=torch.int32)
+    decode(query[:n], cache, out=output[:n], sm_scale=impl.scale, **kw)
     STATS["decode_calls"] += 1
     STATS["decode_tokens"] += n
     return output

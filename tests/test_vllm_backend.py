@@ -276,7 +276,12 @@ def _boundary_plan(monkeypatch, lens, msl=None, host_lens=True, kv=torch.float16
     q = torch.zeros(n, hq, d, dtype=kv)
     kvc = torch.zeros((2, 4, 16, hkv, d), dtype=kv)
     vb.decode_forward(impl, None, q, q, q, kvc, meta, torch.zeros_like(q), decode=fake_decode)
-    return calls[-1]
+    kw = dict(calls[-1])
+    host = kw.pop("seq_lens_host", None)
+    if host is not None:  # a flat launch planned on host lengths also takes them
+        assert host_lens and kw.get("flat_splits") and host.dtype == torch.int32
+        assert host.tolist() == [int(x) for x in lens]
+    return kw
 
 
 def _wrapper_plan(lens, kv="fp16", shape=(32, 8, 128)):
