@@ -149,3 +149,42 @@ def test_impl_forward_large_step_takes_the_flat_split(monkeypatch):
     assert flat_calls and flat_calls[0]
     want = oracle.reference_decode(query, c, out_dtype=torch.float32)
     assert max_abs(output, want) < 2e-3
+
+
+def test_impl_forward_with_host_lengths_passes_them_to_the_flat_split(monkeypatch):
+    """Metadata that carries the lengths on the CPU (`seq_lens_cpu`): the
+    boundary plans on them and hands them to the flat launch, whose ranges
+    and merge list are then built on the host. The output matches the
+    oracle and is byte-equal to the same launch without host lengths."""
+    _, Impl = vb.build_backend_classes(object, _BaseImpl)
+    g = torch.Generator().manual_seed(36)
+    lens = torch.randint(1, 3000, (24,), generator=g).tolist()
+    lens[5] = 2999
+    n = len(lens)
+    c = allocate(LLAMA3_8B, n, lens, seed=36, device="cuda")
+    kv_cache = torch.stack([c.k_cache, c.v_cache])
+    meta = types.SimpleNamespace(max_query_len=1, num_actual_tokens=n, use_cascade=False,
+                                 local_attn_metadata=None, max_seq_len=max(lens),
+                                 block_table=c.block_table, seq_lens=c.seq_lens, slot_mapping=None,
+                                 seq_lens_cpu=torch.tensor(lens, dtype=torch.int32))
+    query = seeded_q(n, 32, 128, 36, device="cuda")
+    output = torch.zeros_like(query)
+    calls = []
+    real_forward, real_decode = vb.decode_forward, vb.paged_decode_triton
+
+    def spy(*a, **kw):
+        calls.append(dict(kw))
+        return real_decode(*a, **kw)
+
+    monkeypatch.setattr(vb, "decode_forward", lambda *a, **kw: real_forward(*a, decode=spy, **kw))
+    Impl(LLAMA3_8B).forward(None, query, None, None, kv_cache, meta, output)
+    torch.cuda.synchronize()
+    kw = calls[-1]
+    print(f"launch {({k: v for k, v in kw.items() if k not in ('seq_lens_host', 'out')})}", flush=True)
+    assert kw.get("flat_splits") and kw["seq_lens_host"].tolist() == lens
+    want = oracle.reference_decode(query, c, out_dtype=torch.float32)
+    assert max_abs(output, want) < 2e-3
+    scan = {k: v for k, v in kw.items() if k not in ("seq_lens_host", "out", "sm_scale")}
+    again = real_decode(query, c, sm_scale=LLAMA3_8B.head_dim ** -0.5, **scan)
+    torch.cuda.synchronize()
+    assert torch.equal(again, output), "host-built tables and the seq_lens scan differ"
