@@ -162,7 +162,9 @@ typedef struct pa_decode_args {
    * the sequences that need it (and is not launched when none do). Launches
    * beyond PA_HOST_TABLE_MAX ranges or merge entries, a batch above 4096 or
    * sequences of 2^25 tokens and more use the GPU scan as without them.
-   * Read during the call only. */
+   * Read during the call only. Ignored while the stream is being captured
+   * into a HIP graph: tables in a graph's kernel arguments would be replayed
+   * with whatever lengths seq_lens then holds, so captured launches scan. */
   const int32_t *seq_lens_host;
 } pa_decode_args;
 

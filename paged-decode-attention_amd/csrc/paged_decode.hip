@@ -1980,6 +1980,30 @@ void build_host_plan(const pa_decode_args *a, const KParams &k, HostPlan *hp) {
   }
 }
 
+// Whether work launched on `st` now is being captured into a HIP graph (an
+// unknown state counts as captured).
+bool stream_capturing(hipStream_t st) {
+  hipStreamCaptureStatus s = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &s) != hipSuccess) {
+    (void)hipGetLastError();
+    return true;
+  }
+  return s != hipStreamCaptureStatusNone;
+}
+
+// The host plan of a launch on `st`. Under HIP graph capture there is none:
+// the tables would be frozen into the graph's kernel arguments while a replay
+// may run on other lengths (a serving loop updates seq_lens in place between
+// replays), so the kernels scan seq_lens, which is right for any lengths.
+void launch_host_plan(const pa_decode_args *a, const KParams &k, HostPlan *hp, hipStream_t st) {
+  if (a->seq_lens_host != nullptr && a->flat_splits > 0 && stream_capturing(st)) {
+    hp->ranges = hp->merge_table = false;
+    hp->needs_merge = true;
+    return;
+  }
+  build_host_plan(a, k, hp);
+}
+
 pa_reduce_args reduce_args_from(const pa_decode_args *a) {
   pa_reduce_args r;
   r.part_out = a->part_out;
@@ -2085,7 +2109,7 @@ int pa_decode(const pa_decode_args *a, void *stream) {
   if (a->batch == 0) return ok();
   hipStream_t st = static_cast<hipStream_t>(stream);
   HostPlan plan;
-  if (flat) build_host_plan(a, k, &plan);
+  if (flat) launch_host_plan(a, k, &plan, st);
   hipError_t e = launch_decode(k, a, flat ? kFlat : split ? kAuto : kUnsplit, st, &plan);
   if (e != hipSuccess) return fail(PA_ERR_HIP, "decode launch failed: %s", hipGetErrorString(e));
   if (split && !(flat && !plan.needs_merge)) {
@@ -2149,7 +2173,7 @@ int pa_decode_partials(const pa_decode_args *a, void *stream) {
   if (rc != PA_OK) return rc;
   if (a->batch == 0) return ok();
   HostPlan plan;
-  if (a->flat_splits > 0) build_host_plan(a, k, &plan);
+  if (a->flat_splits > 0) launch_host_plan(a, k, &plan, static_cast<hipStream_t>(stream));
   hipError_t e = launch_decode(k, a, a->flat_splits > 0 ? kFlat : kPartials,
                                static_cast<hipStream_t>(stream), &plan);
   if (e != hipSuccess) return fail(PA_ERR_HIP, "decode launch failed: %s", hipGetErrorString(e));
@@ -2172,7 +2196,7 @@ int pa_flat_merge(const pa_decode_args *a, void *stream) {
   rp.flat_cost = a->flat_seq_cost;
   if (a->batch == 0) return ok();
   HostPlan plan;
-  build_host_plan(a, k, &plan);
+  launch_host_plan(a, k, &plan, static_cast<hipStream_t>(stream));
   if (!plan.needs_merge) return ok();  // every sequence inside one range: nothing to fold
   hipError_t e;
   if (plan.merge_table) {

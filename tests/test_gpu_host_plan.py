@@ -165,6 +165,44 @@ def test_host_plan_in_a_hip_graph():
         assert torch.equal(out, eager), f"replay with q seed {seed} differs"
 
 
+def test_graph_captured_with_host_lengths_replays_new_lengths():
+    """A serving loop captures a step once and replays it after updating
+    seq_lens in place. The host lengths given at capture are ignored there
+    (the captured kernels scan seq_lens), so every replay equals an eager
+    decode at the lengths seq_lens holds at that replay."""
+    import dataclasses
+
+    lens0 = [300, 1, 1500, 17, 33, 64, 1000, 700]
+    q, c = _case(LLAMA3_8B, lens0, seed=15)
+    live = c.seq_lens
+    host = _host(c)  # read before the capture: no sync may happen inside it
+    out = torch.empty_like(q)
+    kw = {"flat_splits": 29, "flat_seq_cost": 1}
+    paged_decode_hip(q, c, out=out, seq_lens_host=host, **kw)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        paged_decode_hip(q, c, out=out, seq_lens_host=host, **kw)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        paged_decode_hip(q, c, out=out, seq_lens_host=host, **kw)
+    # new lengths within the block table's capacity (each sequence keeps its pages)
+    for lens in ([301, 2, 1501, 18, 34, 64, 1001, 701], [5, 1, 40, 17, 0, 64, 1000, 3],
+                 [300, 1, 1500, 17, 33, 64, 1000, 700]):
+        live.copy_(torch.tensor(lens, dtype=torch.int32))
+        cap = [min(t, c.block_table.shape[1] * c.block_size) for t in lens]
+        assert cap == lens
+        eager = paged_decode_hip(q, dataclasses.replace(c, seq_lens=live.clone()), **kw).clone()
+        torch.cuda.synchronize()
+        out.fill_(7.0)
+        graph.replay()
+        torch.cuda.synchronize()
+        print(f"replay at lengths {lens}", flush=True)
+        assert torch.equal(out, eager), f"replay at lengths {lens} differs from the eager decode"
+
+
 def test_host_plan_rejects_bad_host_lengths():
     q, c = _case(LLAMA3_8B, RAGGED, seed=14)
     for bad in (torch.tensor(RAGGED, dtype=torch.int64), torch.tensor(RAGGED[:3], dtype=torch.int32),
