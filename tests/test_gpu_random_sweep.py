@@ -4,7 +4,8 @@ Each case draws a head geometry, head_dim, KV dtype (with fp16 or fp32 int8
 scales), page size, batch and ragged lengths (empty and 1-token sequences
 included), q/out dtype and a launch shape: unsplit, the reference's
 per-sequence split (with and without `max_seq_len`), the flat split at a random
-range count, or the planner's choice (`num_splits=None`). Every case is held
+range count and per-sequence charge, with or without host-side lengths, or
+the planner's choice (`num_splits=None`). Every case is held
 to the decode's bar against the fp32 oracle (pagedattn/reference.py:28-49
 restated): max |HIP - oracle| < 2e-3 (plus one bf16 rounding for bf16 out),
 and zeros for empty sequences.
@@ -26,7 +27,7 @@ pytestmark = pytest.mark.gpu
 
 ABS_TOL = 2e-3
 GEOMETRIES = [(32, 8), (64, 8), (14, 2), (8, 8), (40, 2), (16, 1), (12, 4), (28, 4)]
-CASES = 48
+CASES = 96
 
 
 def _draw(seed):
@@ -45,7 +46,10 @@ def _draw(seed):
     io = rng.choice([torch.float16, torch.float16, torch.bfloat16])
     mode = rng.choice(["unsplit", "split", "split_msl", "flat", "flat", "auto"])
     knob = rng.randint(2, 9) if mode.startswith("split") else rng.randint(1, 300)
-    return hq, hkv, d, kv, sdt, page, lens, io, mode, knob
+    # drawn last, so the draws above (and the regression cases) are unchanged
+    host = rng.random() < 0.5
+    cost = rng.choice([0, 0, 1, 2, 3])
+    return hq, hkv, d, kv, sdt, page, lens, io, mode, knob, host, cost
 
 
 @pytest.mark.parametrize("case", range(CASES))
@@ -61,9 +65,10 @@ def test_random_regression_case(case):
 
 
 def run_case(case):
-    hq, hkv, d, kv, sdt, page, lens, io, mode, knob = _draw(case)
+    hq, hkv, d, kv, sdt, page, lens, io, mode, knob, host, cost = _draw(case)
     print(f"case {case}: hq={hq} hkv={hkv} d={d} kv={kv} scales={sdt} page={page} "
-          f"B={len(lens)} max_len={max(lens)} io={io} mode={mode} knob={knob}", flush=True)
+          f"B={len(lens)} max_len={max(lens)} io={io} mode={mode} knob={knob} host={host} "
+          f"cost={cost}", flush=True)
     shape = ModelShape(hq, hkv, d, name="sweep")
     c = allocate(shape, len(lens), lens, block_size=page, kv_dtype=kv, seed=case,
                  scale_dtype=sdt, device="cuda")
@@ -76,7 +81,9 @@ def run_case(case):
     elif mode == "split_msl":
         kw.update(num_splits=knob, max_seq_len=max(lens))
     elif mode == "flat":
-        kw["flat_splits"] = knob
+        kw.update(flat_splits=knob, flat_seq_cost=cost)
+        if host:  # the host-built launch tables (and no merge launch when nothing is cut)
+            kw["seq_lens_host"] = torch.tensor(lens, dtype=torch.int32)
     got = paged_decode_hip(q, c, **kw)
     torch.cuda.synchronize()
     want = oracle.reference_decode(q, c, out_dtype=torch.float32)
