@@ -18,7 +18,7 @@ import torch
 
 from . import _abi
 from .cache import PagedKVCache
-from .hip_decode import _call, _stream
+from .hip_decode import _launch
 
 _KV_CODE = {"fp16": _abi.PA_KV_FP16, "fp8_e5m2": _abi.PA_KV_FP8_E5M2, "int8": _abi.PA_KV_INT8,
             "bf16": _abi.PA_KV_BF16}
@@ -88,7 +88,7 @@ def reshape_and_cache(
     else:
         a.scale_dtype = _abi.PA_SCALE_NONE
     lib = _abi.load()
-    rc = _call(key.device, lib.pa_cache_write, ctypes.byref(a), _stream(key.device))
+    rc = _launch(key, lib.pa_cache_write, a)
     _abi.check(rc, "pa_cache_write")
 
 

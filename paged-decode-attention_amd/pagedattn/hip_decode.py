@@ -549,13 +549,15 @@ def _fill_args(
     k, v = cache.k_cache, cache.v_cache
     bt, sl = cache.block_table, cache.seq_lens
     dev = q.get_device()
-    for name, t in (("k_cache", k), ("v_cache", v), ("out", out), ("block_table", bt), ("seq_lens", sl)):
-        if t.get_device() != dev:
-            raise ValueError(f"{name} is on {t.device}, q on {q.device}")
+    if (k.get_device() != dev or v.get_device() != dev or out.get_device() != dev
+            or bt.get_device() != dev or sl.get_device() != dev):
+        for name, t in (("k_cache", k), ("v_cache", v), ("out", out), ("block_table", bt), ("seq_lens", sl)):
+            if t.get_device() != dev:
+                raise ValueError(f"{name} is on {t.device}, q on {q.device}")
     if k.dtype != _STORE_DTYPE[kv_dtype] or v.dtype != k.dtype:
         raise ValueError(f"k/v cache dtype {k.dtype}/{v.dtype} does not match kv_dtype {kv_dtype}")
     kshape, kst = k.shape, k.stride()
-    if len(kshape) != 4 or tuple(kshape[1:]) != (cache.block_size, shape.num_kv_heads, d):
+    if len(kshape) != 4 or kshape[1] != cache.block_size or kshape[2] != shape.num_kv_heads or kshape[3] != d:
         raise ValueError(f"k_cache shape {tuple(kshape)} is not [NB, {cache.block_size}, "
                          f"{shape.num_kv_heads}, {d}]")
     if v.shape != kshape or v.stride() != kst:
@@ -563,12 +565,12 @@ def _fill_args(
     qst, ost = q.stride(), out.stride()
     if kst[3] != 1 or qst[2] != 1 or ost[2] != 1:
         raise ValueError("head_dim must be the contiguous (stride-1) dimension of q, out and the caches")
-    if tuple(out.shape) != (b, hq, d):
+    if out.shape != (b, hq, d):
         raise ValueError(f"out shape {tuple(out.shape)} != {(b, hq, d)}")
     if bt.dtype != torch.int32 or sl.dtype != torch.int32:
         raise ValueError("block_table and seq_lens must be int32")
     btshape, btst = bt.shape, bt.stride()
-    if len(btshape) != 2 or btshape[0] != b or tuple(sl.shape) != (b,):
+    if len(btshape) != 2 or btshape[0] != b or sl.shape != (b,):
         raise ValueError(f"block_table {tuple(btshape)} / seq_lens {tuple(sl.shape)} do not match batch {b}")
     if btst[1] != 1 or sl.stride(0) != 1:
         raise ValueError("block_table rows and seq_lens must be contiguous")
@@ -634,13 +636,21 @@ def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def _call(device: torch.device, fn, *args) -> int:
-    """fn(*args) with `device` current (switching only when it is not)."""
-    idx = device.index
-    if idx is None or idx == torch.cuda.current_device():
-        return fn(*args)
-    with torch.cuda.device(device):
-        return fn(*args)
+_get_device = getattr(torch._C, "_cuda_getDevice", None)
+
+
+def _launch(t: torch.Tensor, fn, args) -> int:
+    """fn(&args, stream) with t's device current, on that device's current
+    torch stream (switching devices only when needed). The per-call path of
+    every wrapper: a device index and the raw stream handle, no device or
+    stream objects."""
+    idx = t.get_device()
+    cur = _get_device() if _get_device is not None else torch.cuda.current_device()
+    if idx == cur:
+        return fn(ctypes.byref(args), _raw_stream(idx) if _raw_stream is not None
+                  else torch.cuda.current_stream(idx).cuda_stream)
+    with torch.cuda.device(idx):
+        return fn(ctypes.byref(args), _stream(torch.device("cuda", idx)))
 
 
 def paged_decode_hip(
@@ -741,10 +751,10 @@ def paged_decode_hip(
     lib = _abi.load()
     if flat > 0 and not merge:
         # every sequence inside one range: the decode pass writes all of out
-        rc = _call(q.device, lib.pa_decode_partials, ctypes.byref(args), _stream(q.device))
+        rc = _launch(q, lib.pa_decode_partials, args)
         _abi.check(rc, "pa_decode_partials")
         return out
-    rc = _call(q.device, lib.pa_decode, ctypes.byref(args), _stream(q.device))
+    rc = _launch(q, lib.pa_decode, args)
     _abi.check(rc, "pa_decode")
     return out
 
@@ -783,7 +793,7 @@ def decode_noalloc(
     args = _fill_args(q, cache, out, 1 if flat else int(num_splits), scale, None, None,
                       int(max_seq_len or 0), flat, int(flat_seq_cost or 0) if flat else 0, seq_lens_host)
     lib = _abi.load()
-    rc = _call(q.device, lib.pa_decode_noalloc, ctypes.byref(args), _stream(q.device))
+    rc = _launch(q, lib.pa_decode_noalloc, args)
     _abi.check(rc, "pa_decode_noalloc")
     return out
 
@@ -829,7 +839,7 @@ def decode_partials(
     args = _fill_args(q, cache, out, num_splits, scale, part_out, part_lse, max_seq_len, flat_splits,
                       flat_seq_cost if flat_splits > 0 else 0, seq_lens_host)
     lib = _abi.load()
-    rc = _call(q.device, lib.pa_decode_partials, ctypes.byref(args), _stream(q.device))
+    rc = _launch(q, lib.pa_decode_partials, args)
     _abi.check(rc, "pa_decode_partials")
     return part_out, part_lse
 
@@ -857,7 +867,7 @@ def flat_merge(
     args = _fill_args(q, cache, out, 1, scale, part_out, part_lse, 0, flat_splits, flat_seq_cost,
                       seq_lens_host)
     lib = _abi.load()
-    rc = _call(q.device, lib.pa_flat_merge, ctypes.byref(args), _stream(q.device))
+    rc = _launch(q, lib.pa_flat_merge, args)
     _abi.check(rc, "pa_flat_merge")
     return out
 
@@ -888,7 +898,7 @@ def split_reduce(
     r.stride_ob, r.stride_oh = out.stride(0), out.stride(1)
     r.io_dtype = _IO_CODE[out.dtype]
     lib = _abi.load()
-    rc = _call(part_out.device, lib.pa_split_reduce, ctypes.byref(r), _stream(part_out.device))
+    rc = _launch(part_out, lib.pa_split_reduce, r)
     _abi.check(rc, "pa_split_reduce")
     return out
 
