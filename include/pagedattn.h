@@ -44,9 +44,11 @@
  * [16, 256]; max_blocks * block_size < 2^31 tokens; batch * stride_btb < 2^31
  * block-table entries; one page
  * (block_size * stride_kt) under 2 GiB and the page stride (stride_kn) under
- * 4 GiB in bytes, likewise 2 GiB / 4 GiB for the int8 scale pages; the pool
- * itself (num_blocks pages) may be any size. q, out, k_cache, v_cache and
- * their strides are 16-byte aligned (PA_ERR_INVALID otherwise).
+ * 4 GiB in bytes, likewise 2 GiB / 4 GiB for the int8 scale pages; the kv-head
+ * stride under 2 GiB in bytes; the q, out and workspace strides under 2^31
+ * elements; the pool itself (num_blocks pages) may be any size. q, out,
+ * k_cache, v_cache and their strides are 16-byte aligned (PA_ERR_INVALID
+ * otherwise).
  */
 #ifndef PAGEDATTN_H_
 #define PAGEDATTN_H_
@@ -57,7 +59,7 @@
 extern "C" {
 #endif
 
-#define PA_ABI_VERSION 7
+#define PA_ABI_VERSION 8
 
 /* Return codes. */
 #define PA_OK 0
@@ -279,22 +281,33 @@ int pa_flat_waves_per_simd(int kv_dtype, int scale_dtype, int head_dim, int *out
  * (split: batch * num_splits, flat: batch + flat_splits slots of
  * num_q_heads * (head_dim + 1) floats) returns PA_ERR_UNSUPPORTED. Every
  * call on one GPU shares that GPU's array, so calls that overlap on one GPU
- * (two streams, two threads) race: the caller serialises them. No
- * counterpart in the reference, whose host wrapper allocates its workspace
- * (pagedattn/triton_decode.py:266-282). */
+ * (two streams, two threads) race: the caller serialises them. The first
+ * call on a device looks up the array's address there (the runtime may load
+ * the code object then), so make one call on each device before capturing
+ * calls into a HIP graph; later calls, captured or not, make no runtime call
+ * besides the launches. No counterpart in the reference; it is for callers
+ * that cannot allocate. */
 int pa_decode_noalloc(const pa_decode_args *args, void *stream);
 
 /* The launch tables pa_decode builds from seq_lens_host for a flat split
  * (flat_splits > 0, seq_lens_host set; the other fields as for pa_decode),
- * computed on the host without any HIP call: ranges[3 j .. 3 j + 2] = range
- * j's first sequence, its first 32-token tile there and its tile count (all
- * zero for a range without tiles); items[3 i .. 3 i + 2] = the i-th sequence
- * the merge writes (cut by a range boundary, or empty), its first partial
- * slot and its slot count (0: empty, zeros), *n_items of them. ranges holds
- * 3 * flat_splits and items 3 * batch int32s. PA_ERR_UNSUPPORTED when the
- * launch is beyond the tables (the kernels then scan seq_lens). No
- * counterpart in the reference; for planners and tests. */
-int pa_flat_host_plan(const pa_decode_args *args, int32_t *ranges, int32_t *items, int32_t *n_items);
+ * computed on the host without any HIP call, complete whatever their size:
+ * ranges[3 j .. 3 j + 2] = range j's first sequence, its first 32-token tile
+ * there and its tile count (all zero for a range without tiles);
+ * items[3 i .. 3 i + 2] = the i-th sequence the merge writes (cut by a range
+ * boundary, or empty), its first partial slot and its slot count (0: empty,
+ * zeros; up to flat_splits), *n_items of them. ranges holds 3 * flat_splits
+ * and items 3 * batch int32s. *in_kernel_args (if not NULL) gets
+ * PA_HOST_PLAN_RANGES when pa_decode passes the ranges to the decode kernel
+ * (at most PA_HOST_TABLE_MAX ranges, a batch up to 4096, block-table rows
+ * of fewer than 2^25 tokens) and PA_HOST_PLAN_MERGE when it passes the merge list to the
+ * merge (at most PA_HOST_TABLE_MAX items); a pass without its table scans
+ * seq_lens on the GPU instead. No counterpart in the reference; for planners
+ * and tests. */
+#define PA_HOST_PLAN_RANGES 1
+#define PA_HOST_PLAN_MERGE 2
+int pa_flat_host_plan(const pa_decode_args *args, int32_t *ranges, int32_t *items, int32_t *n_items,
+                      int32_t *in_kernel_args);
 
 /* Message for the last non-zero return on the calling thread ("" if none). */
 const char *pa_last_error(void);

@@ -115,13 +115,18 @@ struct KParams {
   int32_t batch, max_tokens;  // max_tokens = max_blocks << log2_page
   int32_t flat_splits;        // > 0: the flat (work-balanced) split
   int32_t flat_cost;          // flat split: tiles charged per non-empty sequence
-  int64_t sqb, sqh;          // elements
-  int64_t skn, skt, skh;     // bytes
-  int64_t ssn, sst;          // bytes
-  int64_t sob, soh;          // elements
-  int64_t spb, sph, sps;     // elements
-  int64_t slb, slh;          // elements
-  int64_t sbtb;              // elements
+  // Strides are 32-bit (checked on the host; kernels widen them before they
+  // multiply an index): 64-bit ones took scalar registers the int8 instances
+  // do not have to spare.
+  int32_t sqb, sqh;          // elements
+  uint32_t skn;              // bytes (< 2^32)
+  int32_t skt, skh;          // bytes
+  uint32_t ssn;              // bytes (< 2^32)
+  int32_t sst;               // bytes
+  int32_t sob, soh;          // elements
+  int32_t spb, sph, sps;     // elements
+  int32_t slb, slh;          // elements
+  int32_t sbtb;              // elements
   float qk_scale;            // sm_scale * log2(e)
   int32_t io_bf16;           // q and out are bf16 (else fp16)
 };
@@ -419,22 +424,18 @@ __device__ __forceinline__ void load_tile(Tile<KV, D> &r, const KParams &p, cons
   const uint32_t skt = (uint32_t)p.skt;
   const int page_mask = (1 << p.log2_page) - 1;
 
-  __amdgpu_buffer_rsrc_t rk[NS], rv[NS], rks[NS], rvs[NS];
+  __amdgpu_buffer_rsrc_t rk[NS], rv[NS];
+  uint32_t ph[NS], of[NS];
+  int rows[NS];
 #pragma unroll
   for (int u = 0; u < NS; ++u) {
     const int t0 = min(n0 + 16 * u, (hi - 1) & ~15);
-    const uint32_t ph = (uint32_t)min(max(bt_row[(uint32_t)t0 >> p.log2_page], 0), p.num_blocks - 1);
-    const uint32_t of = (uint32_t)(t0 & page_mask);
-    const int rows = min(hi - t0, 16);  // valid rows of the sub-tile, >= 1
-    const uint64_t row0 = (uint64_t)ph * (uint32_t)p.skn + of * skt;
+    ph[u] = (uint32_t)min(max(bt_row[(uint32_t)t0 >> p.log2_page], 0), p.num_blocks - 1);
+    of[u] = (uint32_t)(t0 & page_mask);
+    rows[u] = min(hi - t0, 16);  // valid rows of the sub-tile, >= 1
+    const uint64_t row0 = (uint64_t)ph[u] * (uint32_t)p.skn + of[u] * skt;
     rk[u] = page_rsrc(ta.k + row0);
-    rv[u] = page_rsrc(ta.v + row0, (int)((uint32_t)rows * skt));
-    if constexpr (KV == PA_KV_INT8) {
-      const uint32_t sst = (uint32_t)p.sst;
-      const uint64_t srow0 = (uint64_t)ph * (uint32_t)p.ssn + of * sst;
-      rks[u] = page_rsrc(ta.ks + srow0);
-      rvs[u] = page_rsrc(ta.vs + srow0, (int)((uint32_t)rows * sst));
-    }
+    rv[u] = page_rsrc(ta.v + row0, (int)((uint32_t)rows[u] * skt));
   }
   if (wait_prev) __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
 
@@ -458,7 +459,18 @@ __device__ __forceinline__ void load_tile(Tile<KV, D> &r, const KParams &p, cons
   if constexpr (KV == PA_KV_INT8) {
     // lane group g = lane / 16 holds scale (K | V)[g / 2] of sub-tile g % 2:
     // four loads, each with a uniform buffer, combined by bit masks (a
-    // select between the loads would become one load from a per-lane buffer)
+    // select between the loads would become one load from a per-lane buffer).
+    // Their buffers are made once the K/V loads are issued, so the two sets
+    // of descriptors are never live together (32 scalar registers at once
+    // pushed the int8 instances past the scalar register file).
+    const uint32_t sst = (uint32_t)p.sst;
+    __amdgpu_buffer_rsrc_t rks[NS], rvs[NS];
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+      const uint64_t srow0 = (uint64_t)ph[u] * (uint32_t)p.ssn + of[u] * sst;
+      rks[u] = page_rsrc(ta.ks + srow0);
+      rvs[u] = page_rsrc(ta.vs + srow0, (int)((uint32_t)rows[u] * sst));
+    }
     const uint32_t k0 = load_scale_bits<SC>(rks[0], ta.s_lane);
     const uint32_t k1 = load_scale_bits<SC>(rks[1], ta.s_lane);
     const uint32_t v0 = load_scale_bits<SC>(rvs[0], ta.s_lane);
@@ -1589,15 +1601,17 @@ __global__ void __launch_bounds__(kMergeWaves * 64) split_reduce_kernel(const RP
 
 // The flat split's merge when the host knows the lengths: a table of the
 // sequences that need it (cut by a range boundary, or empty), so no wave
-// reads seq_lens. Item i: b (bits 0..15) and its slot count S (bits 16..31;
-// 0 = empty, zeros), and its first slot b + j0. Waves take (item, head)
-// pairs in XCD-contiguous order.
+// reads seq_lens. Item i: sequence seq[i], its slot count nslot[i] (0 =
+// empty, zeros; up to the flat split count) and its first slot slot[i] =
+// seq[i] + j0. Waves take (item, head) pairs in XCD-contiguous order.
 struct MergeTable {
   RParams r;
   int32_t items;
-  uint32_t item[kHostTab];
+  uint32_t seq[kHostTab];
+  uint32_t nslot[kHostTab];
   uint32_t slot[kHostTab];
 };
+static_assert(sizeof(MergeTable) <= 4096 && sizeof(FlatArgs) <= 4096, "kernel arguments over 4 KB");
 
 template <int D>
 __global__ void __launch_bounds__(kMergeWaves * 64) flat_merge_table_kernel(const MergeTable a) {
@@ -1614,8 +1628,7 @@ __global__ void __launch_bounds__(kMergeWaves * 64) flat_merge_table_kernel(cons
   if (w >= a.items * p.num_heads) return;
   const int it = w / p.num_heads;
   const int h = w % p.num_heads;
-  const uint32_t e = a.item[it];
-  const int b = (int)(e & 0xffffu), S = (int)(e >> 16);
+  const int b = (int)a.seq[it], S = (int)a.nslot[it];
   const int64_t slot0 = a.slot[it];
   merge_into_out<D>(p, p.part_lse + slot0 * p.slb + (int64_t)h * p.slh,
                     p.part_out + slot0 * p.spb + (int64_t)h * p.sph, p.slb, p.spb, S, b, h, lane,
@@ -1724,10 +1737,18 @@ int build_params(const pa_decode_args *a, bool need_partials, KParams *kp) {
   if (a->stride_kn * elem >= (int64_t(1) << 32))
     return fail(PA_ERR_UNSUPPORTED, "page stride of %lld bytes exceeds 4 GiB",
                 (long long)(a->stride_kn * elem));
+  // the kernels hold the other strides in 32 bits
+  const int64_t big = int64_t(1) << 31;
+  if (a->stride_qb >= big || a->stride_qh >= big || a->stride_ob >= big || a->stride_oh >= big ||
+      a->stride_kh * elem >= big || a->stride_btb >= big)
+    return fail(PA_ERR_UNSUPPORTED, "a q, out, kv-head or block-table stride spans 2^31 elements or bytes");
   if (need_partials) {
     if (a->stride_pb < 0 || a->stride_ph < 0 || a->stride_ps < 0 || a->stride_lb < 0 ||
         a->stride_lh < 0)
       return fail(PA_ERR_INVALID, "workspace strides must be non-negative");
+    if (a->stride_pb >= big || a->stride_ph >= big || a->stride_ps >= big || a->stride_lb >= big ||
+        a->stride_lh >= big)
+      return fail(PA_ERR_UNSUPPORTED, "a workspace stride spans 2^31 elements");
     if (!aligned(a->part_out, 16) || (a->stride_pb * 4) % 16 || (a->stride_ph * 4) % 16 ||
         (a->stride_ps * 4) % 16)
       return fail(PA_ERR_INVALID, "part_out and its strides must be 16-byte aligned");
@@ -1920,7 +1941,18 @@ hipError_t launch_merge_table(const MergeTable &mt, int d, hipStream_t st) {
 // lie in [j * per, (j + 1) * per). Tables that do not fit (more than
 // kHostTab ranges or merge entries, a batch over 4096, sequences of 2^20
 // tiles) are left off and the kernels scan seq_lens.
-void build_host_plan(const pa_decode_args *a, const KParams &k, HostPlan *hp) {
+//
+// `all` (pa_flat_host_plan) receives the complete tables whatever their
+// size: ranges[3 j ..] = (first sequence, first tile, tile count) of range j
+// (3 F entries), items[3 i ..] = (sequence, first slot, slot count) of the
+// i-th sequence the merge writes (3 B entries), and their count.
+struct HostPlanOut {
+  int32_t *ranges;
+  int32_t *items;
+  int32_t n_items;
+};
+
+void build_host_plan(const pa_decode_args *a, const KParams &k, HostPlan *hp, HostPlanOut *all = nullptr) {
   hp->ranges = hp->merge_table = false;
   hp->needs_merge = true;
   if (a->seq_lens_host == nullptr || a->flat_splits <= 0) return;
@@ -1940,44 +1972,61 @@ void build_host_plan(const pa_decode_args *a, const KParams &k, HostPlan *hp) {
     fa.ntab = F;
     for (int j = 0; j < F; ++j) fa.start[j] = fa.ntile[j] = fa.len[j] = 0;
   }
+  if (all != nullptr)
+    for (int j = 0; j < 3 * F; ++j) all->ranges[j] = 0;
   int items = 0;
-  bool fits = B <= 0xffff;
   int64_t cw = 0;
   for (int b = 0; b < B; ++b) {
     const int len = std::max(0, std::min(a->seq_lens_host[b], k.max_tokens));
     const int t = (len + kSplitAlign - 1) / kSplitAlign;
-    int S = 0;
-    int64_t slot = 0;
+    int64_t S = 0, slot = 0;
     if (t > 0) {
       const int64_t first = cw + cost;  // weight of tile 0
       const int64_t j0 = first / per, j1 = (first + t - 1) / per;
-      if (ranges) {
+      if (ranges || all != nullptr) {
         for (int64_t j = j0; j <= j1; ++j) {
           const int64_t lo = std::max(first, j * per), hi = std::min(first + t, (j + 1) * per);
-          if (fa.ntile[j] == 0) {
-            fa.start[j] = ((uint32_t)b << kTabTBits) | (uint32_t)(lo - first);
-            fa.len[j] = (uint32_t)len;
+          if (ranges) {
+            if (fa.ntile[j] == 0) {
+              fa.start[j] = ((uint32_t)b << kTabTBits) | (uint32_t)(lo - first);
+              fa.len[j] = (uint32_t)len;
+            }
+            fa.ntile[j] += (uint32_t)(hi - lo);
           }
-          fa.ntile[j] += (uint32_t)(hi - lo);
+          if (all != nullptr) {
+            int32_t *r = all->ranges + 3 * j;
+            if (r[2] == 0) {
+              r[0] = b;
+              r[1] = (int32_t)(lo - first);
+            }
+            r[2] += (int32_t)(hi - lo);
+          }
         }
       }
       cw += t + cost;
       if (j0 == j1) continue;  // inside one range: the decode pass writes it
-      S = (int)(j1 - j0 + 1);
+      S = j1 - j0 + 1;         // up to F: 32 bits, like the slot index
       slot = b + j0;
     }
-    if (items < kHostTab && fits) {
-      mt.item[items] = (uint32_t)b | ((uint32_t)S << 16);
+    if (items < kHostTab) {
+      mt.seq[items] = (uint32_t)b;
+      mt.nslot[items] = (uint32_t)S;
       mt.slot[items] = (uint32_t)slot;
+    }
+    if (all != nullptr) {
+      all->items[3 * items] = b;
+      all->items[3 * items + 1] = (int32_t)slot;
+      all->items[3 * items + 2] = (int32_t)S;
     }
     ++items;
   }
   hp->ranges = ranges;
   hp->needs_merge = items > 0;
-  if (items <= kHostTab && fits) {
+  if (items <= kHostTab) {
     hp->merge_table = true;
     mt.items = items;
   }
+  if (all != nullptr) all->n_items = items;
 }
 
 // Whether work launched on `st` now is being captured into a HIP graph (an
@@ -2209,7 +2258,8 @@ int pa_flat_merge(const pa_decode_args *a, void *stream) {
   return ok();
 }
 
-int pa_flat_host_plan(const pa_decode_args *a, int32_t *ranges, int32_t *items, int32_t *n_items) {
+int pa_flat_host_plan(const pa_decode_args *a, int32_t *ranges, int32_t *items, int32_t *n_items,
+                      int32_t *in_kernel_args) {
   if (ranges == nullptr || items == nullptr || n_items == nullptr)
     return fail(PA_ERR_INVALID, "ranges, items and n_items must be non-NULL");
   KParams k;
@@ -2218,20 +2268,11 @@ int pa_flat_host_plan(const pa_decode_args *a, int32_t *ranges, int32_t *items, 
   if (a->flat_splits <= 0 || a->seq_lens_host == nullptr)
     return fail(PA_ERR_INVALID, "pa_flat_host_plan needs flat_splits > 0 and seq_lens_host");
   HostPlan plan;
-  build_host_plan(a, k, &plan);
-  if (!plan.ranges || !plan.merge_table)
-    return fail(PA_ERR_UNSUPPORTED, "this launch does not fit the host tables (the kernels scan seq_lens)");
-  for (int j = 0; j < a->flat_splits; ++j) {
-    ranges[3 * j] = (int32_t)(plan.fa.start[j] >> kTabTBits);
-    ranges[3 * j + 1] = (int32_t)(plan.fa.start[j] & kTabTMask);
-    ranges[3 * j + 2] = (int32_t)plan.fa.ntile[j];
-  }
-  *n_items = plan.mt.items;
-  for (int i = 0; i < plan.mt.items; ++i) {
-    items[3 * i] = (int32_t)(plan.mt.item[i] & 0xffffu);
-    items[3 * i + 1] = (int32_t)plan.mt.slot[i];
-    items[3 * i + 2] = (int32_t)(plan.mt.item[i] >> 16);
-  }
+  HostPlanOut all = {ranges, items, 0};
+  build_host_plan(a, k, &plan, &all);
+  *n_items = all.n_items;
+  if (in_kernel_args != nullptr)
+    *in_kernel_args = (plan.ranges ? PA_HOST_PLAN_RANGES : 0) | (plan.merge_table ? PA_HOST_PLAN_MERGE : 0);
   return ok();
 }
 

@@ -12,7 +12,7 @@ import os
 import pathlib
 import threading
 
-PA_ABI_VERSION = 7
+PA_ABI_VERSION = 8
 
 PA_OK = 0
 PA_ERR_INVALID = -1
@@ -37,6 +37,8 @@ PA_MAX_FLAT_SEQ_COST = 64
 PA_NOALLOC_SCRATCH_BYTES = 32 << 20
 PA_MAX_GROUP = 16
 PA_HOST_TABLE_MAX = 256
+PA_HOST_PLAN_RANGES = 1
+PA_HOST_PLAN_MERGE = 2
 
 LIB_NAME = "libpagedattn_hip.so"
 
@@ -198,7 +200,7 @@ def load() -> ctypes.CDLL:
         lib.pa_flat_waves_per_simd.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                                   ctypes.POINTER(ctypes.c_int)]
         lib.pa_flat_waves_per_simd.restype = ctypes.c_int
-        lib.pa_flat_host_plan.argtypes = [ctypes.POINTER(PaDecodeArgs), _vp, _vp, _vp]
+        lib.pa_flat_host_plan.argtypes = [ctypes.POINTER(PaDecodeArgs), _vp, _vp, _vp, _vp]
         lib.pa_flat_host_plan.restype = ctypes.c_int
         lib.pa_last_error.argtypes = []
         lib.pa_last_error.restype = ctypes.c_char_p

@@ -83,7 +83,8 @@ def test_constants_match_header():
     for name in ("PA_ABI_VERSION", "PA_OK", "PA_ERR_INVALID", "PA_ERR_UNSUPPORTED", "PA_ERR_HIP",
                  "PA_KV_FP16", "PA_KV_FP8_E5M2", "PA_KV_INT8", "PA_SCALE_NONE", "PA_SCALE_FP16",
                  "PA_SCALE_FP32", "PA_IO_FP16", "PA_MAX_SPLITS", "PA_MAX_GROUP", "PA_KV_BF16",
-                 "PA_IO_BF16", "PA_MAX_FLAT_SPLITS", "PA_MAX_FLAT_SEQ_COST"):
+                 "PA_IO_BF16", "PA_MAX_FLAT_SPLITS", "PA_MAX_FLAT_SEQ_COST", "PA_HOST_TABLE_MAX",
+                 "PA_HOST_PLAN_RANGES", "PA_HOST_PLAN_MERGE"):
         m = re.search(rf"#define {name} \(?(-?\d+)\)?", text)
         assert m, name
         assert int(m.group(1)) == getattr(_abi, name), name
@@ -152,6 +153,13 @@ INVALID = [
     ("block_table_2pow31", dict(stride_btb=2**30), _abi.PA_ERR_UNSUPPORTED),
     ("scale_page_stride_4gib", dict(kv_dtype=_abi.PA_KV_INT8, scale_dtype=_abi.PA_SCALE_FP32, k_scale=FAKE,
                                     v_scale=FAKE, stride_sn=2**30, stride_st=8), _abi.PA_ERR_UNSUPPORTED),
+    # the other strides are held in 32 bits by the kernels
+    ("q_stride_2pow31", dict(stride_qb=2**31), _abi.PA_ERR_UNSUPPORTED),
+    ("out_stride_2pow31", dict(stride_oh=2**31), _abi.PA_ERR_UNSUPPORTED),
+    ("kv_head_stride_2gib", dict(stride_kh=2**30), _abi.PA_ERR_UNSUPPORTED),
+    ("workspace_stride_2pow31", dict(num_splits=2, part_out=FAKE, part_lse=FAKE, stride_pb=2**31,
+                                     stride_ph=256, stride_ps=128, stride_lb=64, stride_lh=2),
+     _abi.PA_ERR_UNSUPPORTED),
 ]
 
 

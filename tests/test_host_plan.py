@@ -44,15 +44,17 @@ def _args(lens, flat, cost, max_blocks=1 << 12, block_size=16):
     return a, host
 
 
-def _plan(lens, flat, cost, **kw):
+def _plan(lens, flat, cost, with_flags=False, **kw):
     a, host = _args(lens, flat, cost, **kw)
     ranges = (ctypes.c_int32 * (3 * flat))()
     items = (ctypes.c_int32 * (3 * max(1, len(lens))))()
     n = ctypes.c_int32(0)
-    rc = _abi.load().pa_flat_host_plan(ctypes.byref(a), ranges, items, ctypes.byref(n))
+    flags = ctypes.c_int32(-1)
+    rc = _abi.load().pa_flat_host_plan(ctypes.byref(a), ranges, items, ctypes.byref(n), ctypes.byref(flags))
     del host
-    return rc, [tuple(ranges[3 * j:3 * j + 3]) for j in range(flat)], \
-        [tuple(items[3 * i:3 * i + 3]) for i in range(n.value)]
+    got = (rc, [tuple(ranges[3 * j:3 * j + 3]) for j in range(flat)],
+           [tuple(items[3 * i:3 * i + 3]) for i in range(n.value)])
+    return got + (flags.value,) if with_flags else got
 
 
 def _expected(lens, flat, cost, max_tokens):
@@ -104,14 +106,14 @@ def test_host_plan_random_batches():
                 for _ in range(b)]
         flat = rng.choice([1, 2, 5, 37, 128, 256])
         cost = rng.choice([0, 0, 1, 2, 7])
-        rc, ranges, items = _plan(lens, flat, cost)
+        rc, ranges, items, flags = _plan(lens, flat, cost, with_flags=True)
         want_r, want_i = _expected(lens, flat, cost, (1 << 12) * 16)
-        if len(want_i) > _abi.PA_HOST_TABLE_MAX:
-            assert rc == _abi.PA_ERR_UNSUPPORTED
-            continue
         assert rc == _abi.PA_OK
         assert ranges == want_r, (lens, flat, cost)
         assert items == want_i, (lens, flat, cost)
+        # the merge list goes to the kernel only when it fits its table
+        assert bool(flags & _abi.PA_HOST_PLAN_MERGE) == (len(want_i) <= _abi.PA_HOST_TABLE_MAX)
+        assert flags & _abi.PA_HOST_PLAN_RANGES
 
 
 def test_host_plan_clamps_to_the_block_table():
@@ -125,13 +127,43 @@ def test_host_plan_clamps_to_the_block_table():
 
 
 def test_host_plan_limits():
+    """Tables beyond the kernel-argument tables are still reported whole; the
+    flags say which of them pa_decode would pass to the kernels."""
     lens = [100] * 10
-    rc, _, _ = _plan(lens, _abi.PA_HOST_TABLE_MAX + 1, 0)
-    assert rc == _abi.PA_ERR_UNSUPPORTED  # more ranges than the table holds
-    rc, _, _ = _plan([0] * (_abi.PA_HOST_TABLE_MAX + 1), 4, 0)
-    assert rc == _abi.PA_ERR_UNSUPPORTED  # more merge entries than the table holds
-    a, host = _args(lens, 0, 0)
+    flat = _abi.PA_HOST_TABLE_MAX + 1
+    rc, ranges, items, flags = _plan(lens, flat, 0, with_flags=True)
+    assert rc == _abi.PA_OK
+    assert flags == _abi.PA_HOST_PLAN_MERGE  # more ranges than the table holds: the kernels scan
+    want_r, want_i = _expected(lens, flat, 0, (1 << 12) * 16)
+    assert ranges == want_r and items == want_i
+    lens = [0] * (_abi.PA_HOST_TABLE_MAX + 1)
+    rc, ranges, items, flags = _plan(lens, 4, 0, with_flags=True)
+    assert rc == _abi.PA_OK
+    assert flags == _abi.PA_HOST_PLAN_RANGES  # more merge entries than the table holds
+    assert items == [(b, 0, 0) for b in range(len(lens))]
+    a, host = _args([100] * 10, 0, 0)
     ranges = (ctypes.c_int32 * 3)()
     items = (ctypes.c_int32 * 30)()
     n = ctypes.c_int32(0)
-    assert _abi.load().pa_flat_host_plan(ctypes.byref(a), ranges, items, ctypes.byref(n)) == _abi.PA_ERR_INVALID
+    assert _abi.load().pa_flat_host_plan(ctypes.byref(a), ranges, items, ctypes.byref(n), None) == \
+        _abi.PA_ERR_INVALID
+
+
+def test_merge_slot_count_spans_every_range():
+    """One sequence cut by every one of PA_MAX_FLAT_SPLITS ranges: its merge
+    entry counts all of them (the count once lived in 16 bits, where 65,536
+    read as 0 and the merge wrote zeros for the sequence)."""
+    flat = _abi.PA_MAX_FLAT_SPLITS
+    tokens = flat * 32  # one 32-token tile per range
+    rc, ranges, items, flags = _plan([tokens], flat, 0, with_flags=True, max_blocks=tokens // 256,
+                                     block_size=256)
+    assert rc == _abi.PA_OK, _abi.load().pa_last_error()
+    assert items == [(0, 0, flat)]
+    assert ranges == [(0, j, 1) for j in range(flat)]
+    assert flags == _abi.PA_HOST_PLAN_MERGE  # the merge list is passed, the ranges are scanned
+    # past the limit the launch is refused before any table is built
+    a, host = _args([tokens], flat + 1, 0, max_blocks=tokens // 256, block_size=256)
+    r = (ctypes.c_int32 * (3 * (flat + 1)))()
+    it = (ctypes.c_int32 * 3)()
+    n = ctypes.c_int32(0)
+    assert _abi.load().pa_flat_host_plan(ctypes.byref(a), r, it, ctypes.byref(n), None) == _abi.PA_ERR_INVALID

@@ -1,0 +1,96 @@
+"""Register budget of every gfx950 kernel, from the compiler's own report.
+
+The library is compiled for the device (the flags of
+paged-decode-attention_amd/build.py) with `-Rpass-analysis=
+kernel-resource-usage`, which prints, per kernel, its VGPRs, SGPRs, spills
+and private (scratch) segment size. Every kernel must use no scratch and
+spill no register: a scalar-register spill costs a v_readlane in the tile
+loop (int8 tiles are bound by VALU issue), and a private segment makes every
+launch set up scratch memory. CPU only (hipcc cross-compiles).
+"""
+
+from __future__ import annotations
+
+import importlib.util
+import pathlib
+import re
+import shutil
+import subprocess
+import tempfile
+
+import pytest
+
+ROOT = pathlib.Path(__file__).resolve().parent.parent
+PKG = ROOT / "paged-decode-attention_amd"
+
+
+def _build_module():
+    spec = importlib.util.spec_from_file_location("_pa_build_flags", PKG / "build.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def _remarks(src: pathlib.Path, flags: list[str], hipcc: str, tmp: str) -> subprocess.Popen:
+    device_flags = [f for f in flags if f not in ("-shared", "-fPIC")]
+    cmd = [hipcc, *device_flags, f"-I{ROOT / 'include'}", "-c", "--offload-device-only",
+           "-Rpass-analysis=kernel-resource-usage", str(src), "-o", str(pathlib.Path(tmp) / (src.stem + ".o"))]
+    return subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)
+
+
+def parse_resource_remarks(text: str) -> list[dict]:
+    """One dict per kernel: its mangled name and every numeric field of the
+    kernel-resource-usage remarks (VGPRs, TotalSGPRs, ScratchSize [bytes/lane],
+    SGPRs Spill, VGPRs Spill, Occupancy [waves/SIMD], ...)."""
+    kernels, cur = [], None
+    for line in text.splitlines():
+        m = re.search(r"remark: Function Name: (\S+)", line)
+        if m:
+            cur = {"name": m.group(1)}
+            kernels.append(cur)
+            continue
+        m = re.search(r"remark:\s+([A-Za-z][A-Za-z \[\]/]*?): (\d+) \[-Rpass-analysis", line)
+        if m and cur is not None:
+            cur[m.group(1).strip()] = int(m.group(2))
+    return kernels
+
+
+def test_parse_resource_remarks_known_answer():
+    text = "\n".join([
+        "x.hip:1:1: remark: Function Name: _Z1kv [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:1:1: remark:     TotalSGPRs: 106 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:1:1: remark:     VGPRs: 173 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:1:1: remark:     ScratchSize [bytes/lane]: 36 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:1:1: remark:     Dynamic Stack: False [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:1:1: remark:     SGPRs Spill: 16 [-Rpass-analysis=kernel-resource-usage]",
+    ])
+    (k,) = parse_resource_remarks(text)
+    assert k == {"name": "_Z1kv", "TotalSGPRs": 106, "VGPRs": 173, "ScratchSize [bytes/lane]": 36,
+                 "SGPRs Spill": 16}
+
+
+def test_no_kernel_uses_scratch_or_spills():
+    mod = _build_module()
+    hipcc = mod.hipcc()
+    if shutil.which(hipcc) is None and not pathlib.Path(hipcc).exists():
+        pytest.skip("hipcc not available")
+    with tempfile.TemporaryDirectory() as tmp:
+        procs = {src.name: _remarks(src, mod.HIPCC_FLAGS, hipcc, tmp) for src in mod.SOURCES}
+        outs = {name: p.communicate(timeout=900) for name, p in procs.items()}
+    kernels = []
+    for name, (_, err) in outs.items():
+        assert procs[name].returncode == 0, f"{name} failed to compile:\n{err[-2000:]}"
+        got = parse_resource_remarks(err)
+        assert got, f"{name}: no resource remarks"
+        kernels += [(name, k) for k in got]
+    # every decode, merge and cache-write instance of the library
+    assert sum("paged_decode_flat_kernel" in k["name"] for _, k in kernels) == 20
+    assert sum("cache_write_kernel" in k["name"] for _, k in kernels) >= 1
+    bad = [f"{name}: {k['name']} scratch={k.get('ScratchSize [bytes/lane]')} "
+           f"sgpr_spill={k.get('SGPRs Spill')} vgpr_spill={k.get('VGPRs Spill')}"
+           for name, k in kernels
+           if k.get("ScratchSize [bytes/lane]", 0) or k.get("SGPRs Spill", 0) or k.get("VGPRs Spill", 0)]
+    assert not bad, "kernels with scratch or spills:\n" + "\n".join(bad)
+    for name, k in kernels:
+        for field in ("ScratchSize [bytes/lane]", "SGPRs Spill", "VGPRs Spill", "VGPRs"):
+            assert field in k, f"{name}: {k['name']} reports no {field}"
