@@ -16,6 +16,17 @@ C5), each measured the same way in the same process (whole call, decode
 kernel alone, merge alone, HIP-graph whole call, sampled-row parity, bit
 stability, traffic ratio), with C1's CPU baseline on its full 24-row call.
 
+Timing: `us_per_call` (and `value`) is the mean over the --steps timed calls,
+one HIP event pair around them; the same loop is run LOOP_REPEATS more times
+for `us_per_call_median` and `us_per_call_range` (median and extremes of the
+loops' means). The decode kernel alone is timed eagerly and as a replayed
+HIP graph; `kernel_us` is the graph figure for launches that take no host
+launch tables (the captured code path is the same, and the host's launch rate
+cannot set it: C1), else the eager one (a captured flat launch scans
+seq_lens instead of using the host tables). Merge and whole-call graph
+figures are medians of GRAPH_REPLAYS replays after a clock settle; a
+captured flat merge scans seq_lens too.
+
     python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--config c2]
 """
 
@@ -29,6 +40,7 @@ import json
 import math
 import os
 import pathlib
+import statistics
 import sys
 import time
 import types
@@ -529,9 +541,18 @@ def record_sq(paths: list[str]) -> int:
     return 0
 
 
-def _graph_us(fn, calls: int, reps: int) -> float:
-    """µs per call of `fn(i)` for i < calls captured in one HIP graph and
-    replayed `reps` times (no host launch cost in the timed region)."""
+GRAPH_CALLS = 20   # calls captured in one HIP graph
+GRAPH_REPLAYS = 9  # replays timed one by one (the median is reported)
+
+
+def _graph_us(fn, calls: int = GRAPH_CALLS, reps: int = GRAPH_REPLAYS) -> float:
+    """µs per call of `fn(i)` for i < calls captured in one HIP graph: the
+    graph is replayed untimed for CLOCK_SETTLE_S (the capture leaves the GPU
+    idle), then `reps` replays are timed one by one with HIP events and the
+    median replay is divided by `calls` (no host launch cost in the timed
+    region)."""
+    import statistics
+
     import torch
 
     side = torch.cuda.Stream()
@@ -544,17 +565,34 @@ def _graph_us(fn, calls: int, reps: int) -> float:
     with torch.cuda.graph(graph):
         for i in range(calls):
             fn(i)
-    graph.replay()
-    torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ev0.record()
-    for _ in range(reps):
+    settle(lambda i: graph.replay())
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(2 * reps)]
+    for r in range(reps):
+        evs[2 * r].record()
         graph.replay()
-    ev1.record()
+        evs[2 * r + 1].record()
     torch.cuda.synchronize()
-    us = ev0.elapsed_time(ev1) / (calls * reps) * 1e3
+    us = statistics.median(evs[2 * r].elapsed_time(evs[2 * r + 1]) for r in range(reps)) / calls * 1e3
     del graph
     return us
+
+
+LOOP_REPEATS = 6  # extra timed loops of --steps calls, for the median and range
+
+
+def _loop_us(step, n: int, repeats: int) -> list[float]:
+    """µs per call of `repeats` loops of `n` back-to-back calls of `step(i)`,
+    each loop bracketed by one pair of HIP events on the current stream."""
+    import torch
+
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(2 * repeats)]
+    for r in range(repeats):
+        evs[2 * r].record()
+        for i in range(n):
+            step(i)
+        evs[2 * r + 1].record()
+    torch.cuda.synchronize()
+    return [evs[2 * r].elapsed_time(evs[2 * r + 1]) * 1e3 / n for r in range(repeats)]
 
 
 def measure(cfg: str, args, dev, cpu: bool) -> dict:
@@ -655,6 +693,13 @@ def measure(cfg: str, args, dev, cpu: bool) -> dict:
     wall = time.perf_counter() - t_wall
     ms_step = ev0.elapsed_time(ev1) / args.steps
     _log(f"whole call: {ms_step * 1e3:.1f} us/call (wall {wall / args.steps * 1e6:.1f} us/call)")
+    # Spread: the same K-call loop repeated LOOP_REPEATS more times, each
+    # timed by one event pair like the loop above; the median and range of
+    # the loops' per-call means. (An event between every two calls would
+    # time the events as well: it added 2-4 us per call.)
+    loops = [ms_step * 1e3] + _loop_us(step, args.steps, LOOP_REPEATS)
+    dist = {"median": statistics.median(loops), "min": min(loops), "max": max(loops), "loops": len(loops)}
+    _log("loop means: median {median:.2f} us/call, min {min:.2f}, max {max:.2f} over {loops} loops".format(**dist))
 
     # the dominant kernel alone: the decode pass (partials when split)
     if flat:
@@ -675,13 +720,21 @@ def measure(cfg: str, args, dev, cpu: bool) -> dict:
         run(caches[i % copies])
     ev1.record()
     torch.cuda.synchronize()
-    kern_us = ev0.elapsed_time(ev1) / args.steps * 1e3
-    _log(f"decode kernel alone: {kern_us:.1f} us/launch")
+    kern_eager_us = ev0.elapsed_time(ev1) / args.steps * 1e3
+    _log(f"decode kernel alone: {kern_eager_us:.1f} us/launch (eager)")
+    # The same launches replayed as a HIP graph, which the host's launch
+    # rate cannot slow down (it does at C1, whose kernel takes a few us). A
+    # captured flat launch takes no host launch tables (it scans seq_lens),
+    # so for a launch with host tables the eager loop stays the kernel's
+    # figure: it runs the product's code path, and at those sizes the host
+    # keeps ahead of the GPU.
+    kern_graph_us = _graph_us(lambda i: run(caches[i % copies]))
+    _log(f"decode kernel alone: {kern_graph_us:.1f} us/launch (HIP graph)")
+    kern_us = kern_eager_us if host is not None else kern_graph_us
 
     # The merge pass alone. It is a few microseconds of GPU work, less than
     # one Python launch, so back-to-back eager launches would time the host:
     # the launches are captured in a HIP graph and the graph is replayed.
-    inner, outer = 20, max(1, args.steps // 20)
     reduce_us = None
     merge = None
     if flat:
@@ -693,13 +746,14 @@ def measure(cfg: str, args, dev, cpu: bool) -> dict:
         merge(0)
         torch.cuda.synchronize()
         eager = out.clone()
-        reduce_us = _graph_us(merge, inner, outer)
+        reduce_us = _graph_us(merge)
         if not torch.equal(out, eager):
             raise RuntimeError("the merge graph's replay differs from the eager merge")
-        _log(f"merge pass alone: {reduce_us:.2f} us/launch (graph of {inner} launches x {outer})")
+        _log(f"merge pass alone: {reduce_us:.2f} us/launch (graph of {GRAPH_CALLS} launches, median of "
+             f"{GRAPH_REPLAYS} replays; captured, so a flat merge scans seq_lens)")
     # the whole call replayed as a graph: GPU time without the host's
     # launch cost (which dominates C1's eager call)
-    graph_us = _graph_us(step, inner, outer)
+    graph_us = _graph_us(step)
     _log(f"whole call as a HIP graph: {graph_us:.1f} us/call")
 
     ref = oracle.reference_decode(q[rows].cpu(), subset_cache(cache, rows), out_dtype=torch.float32)
@@ -716,6 +770,7 @@ def measure(cfg: str, args, dev, cpu: bool) -> dict:
         "wl": wl, "shape": shape, "splits": splits, "flat": flat, "seq_cost": cost, "launch": launch,
         "copies": copies,
         "us_per_call": ms_step * 1e3, "kernel_us": kern_us, "merge_us": reduce_us, "graph_us": graph_us,
+        "kernel_eager_us": kern_eager_us, "kernel_graph_us": kern_graph_us, "dist": dist,
         "algo": algo, "kv_bytes": cache.bytes_read_per_decode_step(), "max_abs": max_abs, "rel": rel,
         "rows": rows, "bit_stable": bit_stable, "kernel_name": kernel_name, "traffic": traffic,
         "traffic_note": traffic_note,
@@ -740,8 +795,12 @@ def summary(r: dict) -> dict:
         "workload": wl.description,
         "launch": r["launch"],
         "us_per_call": round(r["us_per_call"], 2),
+        "us_per_call_median": round(r["dist"]["median"], 2),
+        "us_per_call_range": [round(r["dist"]["min"], 2), round(r["dist"]["max"], 2)],
         "graph_us_per_call": round(r["graph_us"], 2),
         "kernel_us": round(r["kernel_us"], 2),
+        "kernel_eager_us": round(r["kernel_eager_us"], 2),
+        "kernel_graph_us": round(r["kernel_graph_us"], 2),
         "merge_us": None if r["merge_us"] is None else round(r["merge_us"], 2),
         "algorithmic_bytes": algo,
         "gbs": round(algo / (r["us_per_call"] * 1e-6) / 1e9, 1),
@@ -850,6 +909,9 @@ def main() -> int:
         "value": round(value, 2),
         "unit": "GB/s",
         "us_per_call": round(h["us_per_call"], 2),
+        "us_per_call_median": round(h["dist"]["median"], 2),
+        "us_per_call_range": [round(h["dist"]["min"], 2), round(h["dist"]["max"], 2)],
+        "timed_loops": h["dist"]["loops"],
         "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "n_gpus": 1,
         "steps": args.steps,
@@ -890,6 +952,8 @@ def main() -> int:
             "traffic": h["traffic"],
             "kernel": h["kernel_name"],
             "kernel_us": round(h["kernel_us"], 2),
+            "kernel_eager_us": round(h["kernel_eager_us"], 2),
+            "kernel_graph_us": round(h["kernel_graph_us"], 2),
         },
         "cpu_baseline": h.get("cpu_baseline"),
     }

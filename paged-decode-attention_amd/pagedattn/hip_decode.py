@@ -19,6 +19,7 @@ from __future__ import annotations
 import ctypes
 import dataclasses
 import threading
+import weakref
 
 import torch
 
@@ -524,6 +525,16 @@ def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+# Validated argument structs, keyed by everything their validation read
+# except the per-call pointers (q, out, workspace, host lengths). The cache
+# object and its tensors enter the key by identity and data pointer and are
+# held by weak references, so a key cannot match a new object that reuses a
+# dead one's id; replacing a tensor or its storage validates again. A tensor
+# reshaped in place on the same memory (resize_, set_) is not noticed.
+_ARG_TEMPLATES: dict[tuple, tuple] = {}
+_ARG_TEMPLATES_MAX = 512
+
+
 def _fill_args(
     q: torch.Tensor,
     cache: PagedKVCache,
@@ -537,6 +548,64 @@ def _fill_args(
     flat_seq_cost: int = 0,
     seq_lens_host: torch.Tensor | None = None,
 ) -> _abi.PaDecodeArgs:
+    """The pa_decode_args of one call: validated on the first call of its
+    geometry (`_pack_args`), afterwards a copy of that struct with this
+    call's pointers (the C side validates every call again)."""
+    k, v, bt, sl = cache.k_cache, cache.v_cache, cache.block_table, cache.seq_lens
+    ks, vs = cache.k_scale, cache.v_scale
+    shape = cache.shape
+    key = (id(cache), id(k), k.data_ptr(), id(v), v.data_ptr(), id(bt), bt.data_ptr(), id(sl),
+           sl.data_ptr(), id(ks), 0 if ks is None else ks.data_ptr(), id(vs), 0 if vs is None else vs.data_ptr(),
+           cache.kv_dtype, cache.block_size, shape.num_q_heads, shape.num_kv_heads, shape.head_dim,
+           q.shape, q.stride(), q.dtype, q.get_device(), out.shape, out.stride(), out.dtype,
+           out.get_device(), num_splits, sm_scale, max_seq_len, flat_splits, flat_seq_cost,
+           None if part_out is None else (part_out.shape, part_out.stride(), part_out.dtype,
+                                          part_out.get_device(), part_lse.shape, part_lse.stride(),
+                                          part_lse.dtype, part_lse.get_device()),
+           seq_lens_host is None)
+    hit = _ARG_TEMPLATES.get(key)
+    objs = (cache, k, v, bt, sl, ks, vs)
+    if hit is not None and all(r is None or r() is o for r, o in zip(hit[0], objs)):
+        if seq_lens_host is not None and flat_splits > 0:
+            _check_host_lens(seq_lens_host, q.shape[0])
+        a = _abi.PaDecodeArgs.from_buffer_copy(hit[1])
+        a.q = q.data_ptr()
+        a.out = out.data_ptr()
+        if part_out is not None:
+            a.part_out = part_out.data_ptr()
+            a.part_lse = part_lse.data_ptr()
+        if seq_lens_host is not None and flat_splits > 0:
+            a.seq_lens_host = seq_lens_host.data_ptr()
+        return a
+    tmpl = _pack_args(q, cache, out, num_splits, sm_scale, part_out, part_lse, max_seq_len,
+                      flat_splits, flat_seq_cost, seq_lens_host)
+    if len(_ARG_TEMPLATES) >= _ARG_TEMPLATES_MAX:
+        _ARG_TEMPLATES.clear()
+    refs = tuple(None if o is None else weakref.ref(o) for o in objs)
+    _ARG_TEMPLATES[key] = (refs, tmpl)
+    return _abi.PaDecodeArgs.from_buffer_copy(tmpl)
+
+
+def _check_host_lens(seq_lens_host: torch.Tensor, b: int) -> None:
+    if (seq_lens_host.device.type != "cpu" or seq_lens_host.dtype != torch.int32
+            or tuple(seq_lens_host.shape) != (b,) or not seq_lens_host.is_contiguous()):
+        raise ValueError(f"seq_lens_host must be a contiguous int32 CPU tensor of shape ({b},)")
+
+
+def _pack_args(
+    q: torch.Tensor,
+    cache: PagedKVCache,
+    out: torch.Tensor,
+    num_splits: int,
+    sm_scale: float,
+    part_out: torch.Tensor | None,
+    part_lse: torch.Tensor | None,
+    max_seq_len: int = 0,
+    flat_splits: int = 0,
+    flat_seq_cost: int = 0,
+    seq_lens_host: torch.Tensor | None = None,
+) -> _abi.PaDecodeArgs:
+    """Validate every tensor of a call and pack pa_decode_args."""
     b, hq, d = q.shape
     shape = cache.shape
     kv_dtype = cache.kv_dtype
@@ -608,9 +677,7 @@ def _fill_args(
 
     host_ptr = None
     if seq_lens_host is not None and flat_splits > 0:
-        if (seq_lens_host.device.type != "cpu" or seq_lens_host.dtype != torch.int32
-                or tuple(seq_lens_host.shape) != (b,) or not seq_lens_host.is_contiguous()):
-            raise ValueError(f"seq_lens_host must be a contiguous int32 CPU tensor of shape ({b},)")
+        _check_host_lens(seq_lens_host, b)
         host_ptr = seq_lens_host.data_ptr()
 
     # one constructor call, fields in declaration order (include/pagedattn.h)

@@ -56,3 +56,29 @@ def subset_cache(cache, rows):
         block_table=torch.stack(sel_bt),
         seq_lens=torch.tensor(sel_lens, dtype=torch.int32),
     )
+
+
+def golden_case(path):
+    """(q, cache, sm_scale, npz) of a fixture written by tests/golden/make_golden.py:
+    the reference's NHD cache and fp16 q as CPU tensors (the raw bytes, viewed
+    back as their types), the fixture's softmax scale, and the open npz (its
+    float64 `out`, and `part` / `lse2` / `num_splits` where present)."""
+    import numpy as np
+
+    from pagedattn import ModelShape, PagedKVCache
+
+    z = np.load(path, allow_pickle=False)
+    kv_dtype = str(z["kv_dtype"])
+    sd = {"fp16": torch.float16, "fp32": torch.float32}.get(str(z["scale_dtype"]))
+    store = {"fp16": torch.float16, "fp8_e5m2": torch.float8_e5m2, "int8": torch.int8}[kv_dtype]
+    as_t = lambda a, dt: torch.from_numpy(a.copy()).view(dt)
+    hq, hkv, d = (int(x) for x in z["heads"])
+    shape = ModelShape(hq, hkv, d, "golden")
+    k = as_t(z["k_cache"], store)
+    v = as_t(z["v_cache"], store)
+    ks = as_t(z["k_scale"], sd) if sd is not None else None
+    vs = as_t(z["v_scale"], sd) if sd is not None else None
+    c = PagedKVCache(shape, int(z["block_size"]), kv_dtype, k, v, ks, vs,
+                     torch.from_numpy(z["block_table"].copy()), torch.from_numpy(z["seq_lens"].copy()))
+    q = torch.from_numpy(z["q"].copy()).view(torch.float16)
+    return q, c, float(z["sm_scale"]), z

@@ -10,8 +10,13 @@ depend on size:
   * moving every page to another physical block and rewriting the block
     table leaves the output bit-identical (the reference's shuffle test,
     test_correctness.py:100-110, at pool scale);
-and the CPU oracle (pagedattn/reference.py:28-49 restated) checks the first
-and last sequences within max |HIP - oracle_fp32| < 2e-3.
+and the CPU oracle (pagedattn/reference.py:28-49 restated) checks the first,
+middle and last sequences and five seeded others within max |HIP -
+oracle_fp32| < 2e-3. The launch checked against the oracle is the one the
+product makes (the planner's flat split with host launch tables: C3 with a
+per-sequence charge of 2 tiles, C4 at two waves per SIMD), the launch the
+reference's own full-batch tests exercise through `paged_decode_triton`
+(tests/test_correctness.py:54-61, 100-110, 162-174).
 """
 
 from __future__ import annotations
@@ -24,7 +29,7 @@ import torch
 
 from helpers import max_abs, seeded_q, subset_cache
 from oracle import reference as oracle
-from pagedattn import LLAMA3_8B, LLAMA3_70B, allocate, flat_splits_for, flat_waves_per_simd
+from pagedattn import LLAMA3_8B, LLAMA3_70B, allocate, flat_splits_for, flat_waves_per_simd, plan_launch
 from pagedattn.hip_decode import _cu_count, paged_decode_hip, pick_num_splits
 
 pytestmark = pytest.mark.gpu
@@ -59,34 +64,73 @@ def _build(cfg, seed):
     return q, cache, lens
 
 
+def _product_plan(c, lens, dev):
+    """The launch the product makes for this batch: `plan_launch` with the
+    lengths, the KV dtype and head_dim (what paged_decode_hip(num_splits=None)
+    and bench.py use)."""
+    shape = c.shape
+    wps = flat_waves_per_simd(c.kv_dtype, shape.head_dim, None if c.k_scale is None else c.k_scale.dtype)
+    return plan_launch(len(lens), 0, shape.num_kv_heads, shape.gqa_group, _cu_count(dev), wps,
+                       kv_dtype=c.kv_dtype, head_dim=shape.head_dim, seq_lens=lens)
+
+
+# the launch each config takes on a 256-CU MI355X (checked when the GPU has 256 CUs)
+EXPECTED_PLAN = {
+    "c2": dict(flat_splits=128, flat_seq_cost=0),
+    "c3": dict(flat_splits=128, flat_seq_cost=2),
+    "c4": dict(flat_splits=256, flat_seq_cost=0),  # int8: two waves per SIMD
+    "c5": dict(flat_splits=128, flat_seq_cost=0),
+}
+
+
 @pytest.mark.parametrize("cfg", ["c2", "c3", "c4", "c5"])
 def test_launch_shapes_agree_at_full_size(cfg):
     q, c, lens = _build(cfg, seed=31)
     shape = c.shape
     dev = q.device
-    wps = flat_waves_per_simd(c.kv_dtype, shape.head_dim, None if c.k_scale is None else c.k_scale.dtype)
-    flat = flat_splits_for(shape.num_kv_heads, shape.gqa_group, _cu_count(dev), wps)
+    plan = _product_plan(c, lens, dev)
+    if _cu_count(dev) == 256:
+        assert plan.launch_kwargs() == EXPECTED_PLAN[cfg], plan
+    host = torch.tensor(lens, dtype=torch.int32)
     # the reference's per-sequence split, at least two pieces per sequence
     splits = max(2, pick_num_splits(len(lens), shape.num_kv_heads, max(lens), _cu_count(dev)))
-    print(f"{cfg}: flat={flat} classic splits={splits}", flush=True)
+    print(f"{cfg}: product launch {plan.launch_kwargs()} merge={plan.merge}, classic splits={splits}",
+          flush=True)
 
-    a = paged_decode_hip(q, c, flat_splits=flat).clone()
-    b = paged_decode_hip(q, c, flat_splits=flat)
+    # the product's launch: planner's shape, host launch tables
+    a = paged_decode_hip(q, c, seq_lens_host=host, **plan.launch_kwargs()).clone()
+    b = paged_decode_hip(q, c, seq_lens_host=host, **plan.launch_kwargs())
     torch.cuda.synchronize()
-    assert torch.equal(a, b), "flat split not bit-stable"
+    assert torch.equal(a, b), "product launch not bit-stable"
+    # paged_decode_hip(num_splits=None) plans the same launch itself
+    auto = paged_decode_hip(q, c)
+    torch.cuda.synchronize()
+    assert torch.equal(a, auto), "num_splits=None differs from the planner's launch"
+    # the same ranges scanned on the GPU (a captured launch takes no host tables)
+    scan = paged_decode_hip(q, c, **plan.launch_kwargs())
+    torch.cuda.synchronize()
+    assert torch.equal(a, scan), "host launch tables and the seq_lens scan differ"
     classic = paged_decode_hip(q, c, num_splits=splits, max_seq_len=max(lens)).clone()
     unsplit = paged_decode_hip(q, c, num_splits=1).clone()
     torch.cuda.synchronize()
     d_classic = (a.float() - classic.float()).abs().max().item()
     d_unsplit = (a.float() - unsplit.float()).abs().max().item()
-    print(f"{cfg}: max |flat - classic| = {d_classic:.2e}, |flat - unsplit| = {d_unsplit:.2e}", flush=True)
+    print(f"{cfg}: max |product - classic| = {d_classic:.2e}, |product - unsplit| = {d_unsplit:.2e}",
+          flush=True)
     assert d_classic < ABS_TOL and d_unsplit < ABS_TOL
 
-    rows = [0, len(lens) - 1]
-    want = oracle.reference_decode(q[rows].cpu(), subset_cache(c, rows), out_dtype=torch.float32)
-    err = max_abs(a[rows], want)
-    print(f"{cfg}: rows {rows} max_abs vs oracle = {err:.2e}", flush=True)
-    assert err < ABS_TOL
+    # the oracle on the first, middle and last sequences and five seeded others
+    n = len(lens)
+    g = torch.Generator().manual_seed(1000 + n)
+    extra = torch.randperm(n, generator=g).tolist()
+    rows = sorted({0, n // 2, n - 1} | set([r for r in extra if r not in (0, n // 2, n - 1)][:5]))
+    # C5's rows each hold 4 GiB of fp32 K/V in the oracle: two at a time
+    for part in ([rows] if cfg != "c5" else [rows[i:i + 2] for i in range(0, len(rows), 2)]):
+        want = oracle.reference_decode(q[part].cpu(), subset_cache(c, part), out_dtype=torch.float32)
+        err = max_abs(a[part], want)
+        rel = err / want.abs().max().item()
+        print(f"{cfg}: rows {part} max_abs vs oracle = {err:.2e} rel {rel:.2e}", flush=True)
+        assert err < ABS_TOL and rel < 1e-2
 
 
 def test_page_moves_leave_output_bit_identical_at_full_size():

@@ -23,6 +23,7 @@ import numpy as np
 import pytest
 import torch
 
+from helpers import golden_case
 from oracle import c_oracle
 from oracle import reference as oracle
 from pagedattn import LLAMA3_8B, MHA_DEBUG, ModelShape, allocate
@@ -541,32 +542,13 @@ def _golden_files():
     return sorted(GOLDEN.glob("*.npz"))
 
 
-def _cache_from_npz(z):
-    kv_dtype = str(z["kv_dtype"])
-    sd = {"fp16": torch.float16, "fp32": torch.float32}.get(str(z["scale_dtype"]))
-    store = {"fp16": torch.float16, "fp8_e5m2": torch.float8_e5m2, "int8": torch.int8}[kv_dtype]
-    as_t = lambda a, dt: torch.from_numpy(a.copy()).view(dt)
-    hq, hkv, d = (int(x) for x in z["heads"])
-    shape = ModelShape(hq, hkv, d, "golden")
-    k = as_t(z["k_cache"], store)
-    v = as_t(z["v_cache"], store)
-    ks = as_t(z["k_scale"], sd) if sd is not None else None
-    vs = as_t(z["v_scale"], sd) if sd is not None else None
-    c = PagedKVCache(shape, int(z["block_size"]), kv_dtype, k, v, ks, vs,
-                     torch.from_numpy(z["block_table"].copy()), torch.from_numpy(z["seq_lens"].copy()))
-    q = torch.from_numpy(z["q"].copy()).view(torch.float16)
-    return q, c
-
-
 def test_golden_fixtures_present():
     assert len(_golden_files()) >= 4
 
 
 @pytest.mark.parametrize("path", _golden_files(), ids=lambda p: p.stem)
 def test_golden_fixture(path):
-    z = np.load(path, allow_pickle=False)
-    q, c = _cache_from_npz(z)
-    sm = float(z["sm_scale"])
+    q, c, sm, z = golden_case(path)
     want = torch.from_numpy(z["out"])
     got = oracle.reference_decode(q, c, sm_scale=sm, out_dtype=torch.float32)
     assert (got.double() - want).abs().max().item() < 2e-5
