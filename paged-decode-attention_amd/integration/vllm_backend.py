@@ -145,12 +145,46 @@ def _cu_count(device: torch.device) -> int:
 
 
 def _host_seq_lens(attn_metadata, n: int):
-    """The step's lengths as host ints when the metadata holds a CPU copy
-    (`seq_lens_cpu`, as newer vLLM common metadata does), else None."""
+    """The step's lengths as a contiguous int32 CPU tensor when the metadata
+    holds a CPU copy (`seq_lens_cpu`, as newer vLLM common metadata does),
+    else None. The kernels trust it to equal `seq_lens` (a stale copy would
+    attend over the wrong tokens); with PAGEDATTN_CHECK_HOST_LENS=1 every new
+    step compares the two (one device sync) and raises if they differ."""
     t = getattr(attn_metadata, "seq_lens_cpu", None)
-    if isinstance(t, torch.Tensor) and t.device.type == "cpu":
-        return t[:n].tolist()
-    return None
+    if not (isinstance(t, torch.Tensor) and t.device.type == "cpu"):
+        return None
+    t = t[:n]
+    if t.dtype != torch.int32 or not t.is_contiguous():
+        t = t.to(torch.int32).contiguous()
+    if os.environ.get("PAGEDATTN_CHECK_HOST_LENS") == "1":
+        dev = attn_metadata.seq_lens[:n].to("cpu", torch.int32)
+        if not torch.equal(dev, t):
+            raise ValueError("attn_metadata.seq_lens_cpu differs from seq_lens: the host lengths "
+                             "the decode would plan and launch from are stale")
+    return t
+
+
+# The plan of the current decode step. Every attention layer of a step gets
+# the same metadata object, so the plan (and the host lengths view) is made
+# once per step, not once per layer: planning a ragged batch of 256 cost
+# ~0.1 ms, per layer. The key holds the metadata itself (one object, the last
+# step's), the step's sizes and the layer geometry.
+_STEP_PLAN: list = [None]
+
+
+def _step_plan(attn_metadata, n: int, impl, kv_dtype: str, device: torch.device):
+    msl = int(attn_metadata.max_seq_len)
+    key = (id(attn_metadata.seq_lens), n, msl, impl.num_kv_heads, impl.num_heads, impl.head_size,
+           kv_dtype, device)
+    hit = _STEP_PLAN[0]
+    if hit is not None and hit[0] is attn_metadata and hit[1] == key:
+        return hit[2], hit[3]
+    host = _host_seq_lens(attn_metadata, n)
+    plan = plan_launch(n, msl, impl.num_kv_heads, impl.num_heads // impl.num_kv_heads, _cu_count(device),
+                       flat_waves_per_simd(kv_dtype, impl.head_size), kv_dtype=kv_dtype,
+                       head_dim=impl.head_size, seq_lens=host)
+    _STEP_PLAN[0] = (attn_metadata, key, plan, host)
+    return plan, host
 
 
 def decode_forward(impl, layer, query, key, value, kv_cache, attn_metadata, output,
@@ -179,14 +213,10 @@ def decode_forward(impl, layer, query, key, value, kv_cache, attn_metadata, outp
     # otherwise it plans for a ragged batch of up to max_seq_len tokens.
     # A flat launch planned on host lengths also takes them (its ranges and
     # merge list are then built on the host).
-    msl = int(attn_metadata.max_seq_len)
-    host = _host_seq_lens(attn_metadata, n)
-    plan = plan_launch(n, msl, impl.num_kv_heads, impl.num_heads // impl.num_kv_heads,
-                       _cu_count(query.device), flat_waves_per_simd(cache.kv_dtype, impl.head_size),
-                       kv_dtype=cache.kv_dtype, head_dim=impl.head_size, seq_lens=host)
+    plan, host = _step_plan(attn_metadata, n, impl, cache.kv_dtype, query.device)
     kw = plan.launch_kwargs()
     if plan.flat_splits and host is not None:
-        kw["seq_lens_host"] = torch.tensor(host, dtype=torch.int32)
+        kw["seq_lens_host"] = host
     decode(query[:n], cache, out=output[:n], sm_scale=impl.scale, **kw)
     STATS["decode_calls"] += 1
     STATS["decode_tokens"] += n

@@ -21,6 +21,7 @@ import dataclasses
 import threading
 import weakref
 
+import numpy as np
 import torch
 
 from . import _abi
@@ -184,14 +185,34 @@ def pick_num_splits(
     return int(max(1, min(want, max_useful, _abi.PA_MAX_SPLITS)))
 
 
-def _nearly_uniform(lens: list[int]) -> bool:
+def _lens_array(seq_lens) -> np.ndarray:
+    """Host lengths (ints, a CPU tensor or an array) as int64, negatives as 0.
+    The planners work on whole arrays: a serving step plans batches of
+    hundreds of sequences, and a Python loop per length cost ~0.4 ms at 256."""
+    if isinstance(seq_lens, torch.Tensor):
+        arr = seq_lens.detach().cpu().numpy()
+    else:
+        arr = np.asarray(seq_lens)
+    return np.maximum(arr.astype(np.int64, copy=False).reshape(-1), 0)
+
+
+def _tiles_array(lens: np.ndarray) -> np.ndarray:
+    return (lens + (TILE_TOKENS - 1)) // TILE_TOKENS
+
+
+def _nearly_uniform(lens) -> bool:
     """Longest length at most 1.25 x the mean (a non-empty batch)."""
-    return bool(lens) and max(lens) > 0 and max(lens) <= 1.25 * sum(lens) / len(lens)
+    lens = _lens_array(lens)
+    if lens.size == 0:
+        return False
+    tmax = int(lens.max())
+    return tmax > 0 and tmax <= 1.25 * int(lens.sum()) / lens.size
 
 
-def _fills_unsplit(lens: list[int], num_kv_heads: int, group: int, sm_count: int) -> bool:
+def _fills_unsplit(lens, num_kv_heads: int, group: int, sm_count: int) -> bool:
     """A nearly uniform batch whose unsplit workgroups already give every CU one."""
-    return _nearly_uniform(lens) and len(lens) * _units(num_kv_heads, group) >= max(1, sm_count)
+    lens = _lens_array(lens)
+    return _nearly_uniform(lens) and lens.size * _units(num_kv_heads, group) >= max(1, sm_count)
 
 
 def short_batch_runs_unsplit(batch: int, max_seq_len: int, num_kv_heads: int, group: int,
@@ -232,15 +253,15 @@ def plan_num_splits(seq_lens, num_kv_heads: int, group: int, sm_count: int) -> t
         RAGGED_SPLIT_MIN_TILES tiles, else about four rounds of workgroups,
         chunk ~ sum(T) * heads / (4 CUs).
     """
-    lens = [max(0, int(t)) for t in seq_lens]
-    if not lens or max(lens) == 0:
+    lens = _lens_array(seq_lens)
+    if lens.size == 0 or int(lens.max()) == 0:
         return 1, 0
-    tmax = max(lens)
+    tmax = int(lens.max())
     units = _units(num_kv_heads, group)
     if _fills_unsplit(lens, num_kv_heads, group, sm_count) or _tiles(tmax) <= UNSPLIT_MAX_TILES:
         return 1, tmax
-    work, cus = sum(lens) * units, max(1, sm_count)
-    if len(lens) * units >= cus:
+    work, cus = int(lens.sum()) * units, max(1, sm_count)
+    if lens.size * units >= cus:
         # every CU has a workgroup already (a ragged batch): split only long
         # sequences, into several rounds of workgroups
         if _tiles(tmax) <= RAGGED_SPLIT_MIN_TILES:
@@ -321,11 +342,11 @@ def plan_launch(batch: int, max_seq_len: int, num_kv_heads: int, group: int, sm_
     """
     cus = max(1, sm_count)
     known = seq_lens is not None
-    lens = [max(0, int(t)) for t in seq_lens] if known else None
+    lens = _lens_array(seq_lens) if known else None
     if known:
-        batch = len(lens)
-        tmax = max(lens) if lens else 0
-        tiles = sum(_tiles(t) for t in lens)
+        batch = int(lens.size)
+        tmax = int(lens.max()) if batch else 0
+        tiles = int(_tiles_array(lens).sum())
     else:
         tmax = max(0, int(max_seq_len))
         tiles = batch * _tiles(tmax)  # an upper bound
@@ -341,7 +362,7 @@ def plan_launch(batch: int, max_seq_len: int, num_kv_heads: int, group: int, sm_
             if short_batch_runs_unsplit(batch, tmax, num_kv_heads, group, cus, kv_dtype,
                                         uniform=fills):
                 return LaunchPlan(1, tmax, 0)
-            kv_bytes = sum(lens) * num_kv_heads * head_dim * _KV_ELEM_BYTES.get(kv_dtype, 2) * 2 \
+            kv_bytes = int(lens.sum()) * num_kv_heads * head_dim * _KV_ELEM_BYTES.get(kv_dtype, 2) * 2 \
                 if known else 0
             limit = UNSPLIT_MAX_KV_BYTES_PER_CU.get(kv_dtype, 0) * cus
             if fills and kv_bytes <= limit and merge:
@@ -349,7 +370,8 @@ def plan_launch(batch: int, max_seq_len: int, num_kv_heads: int, group: int, sm_
         return LaunchPlan(1, tmax, flat, merge, cost)
     # the classic split, planned on the lengths (unknown: every sequence as
     # long as the longest, which sizes the chunks for the worst case)
-    splits, tmax = plan_num_splits(lens if known else [tmax] * batch, num_kv_heads, group, cus)
+    splits, tmax = plan_num_splits(lens if known else np.full(batch, tmax, dtype=np.int64),
+                                   num_kv_heads, group, cus)
     return LaunchPlan(splits, tmax, 0)
 
 
@@ -358,8 +380,8 @@ def plan_decode(seq_lens, num_kv_heads: int, group: int, sm_count: int,
                 head_dim: int | None = None) -> tuple[int, int, int]:
     """(num_splits, max_seq_len, flat_splits) for a batch whose lengths the
     host knows: `plan_launch` with the lengths."""
-    lens = list(seq_lens)
-    p = plan_launch(len(lens), 0, num_kv_heads, group, sm_count, waves_per_simd, kv_dtype,
+    lens = _lens_array(seq_lens)
+    p = plan_launch(int(lens.size), 0, num_kv_heads, group, sm_count, waves_per_simd, kv_dtype,
                     head_dim, seq_lens=lens)
     return p.num_splits, p.max_seq_len, p.flat_splits
 
@@ -377,22 +399,19 @@ def flat_needs_merge(seq_lens, flat_splits: int, max_tokens: int | None = None,
     launch's flat_seq_cost: a non-empty sequence weighs its tiles plus
     `seq_cost`, and the ranges take equal weight.
     """
-    lens = [max(0, int(t)) for t in seq_lens]
+    lens = _lens_array(seq_lens)
     if max_tokens is not None:
-        lens = [min(t, max_tokens) for t in lens]
-    tiles = [_tiles(t) for t in lens]
-    weights = [n + seq_cost if n else 0 for n in tiles]
-    total = sum(weights)
+        lens = np.minimum(lens, max_tokens)
+    tiles = _tiles_array(lens)
+    weights = np.where(tiles > 0, tiles + seq_cost, 0)
+    total = int(weights.sum())
     if total == 0 or flat_splits <= 0:
         return True
+    if bool((tiles == 0).any()):
+        return True  # the merge writes an empty sequence's zeros
     per = max(1, -(-total // flat_splits))
-    cw = 0
-    for n, w in zip(tiles, weights):
-        first = cw + seq_cost  # weight of the sequence's tile 0
-        if n == 0 or first // per != (first + n - 1) // per:
-            return True
-        cw += w
-    return False
+    first = np.cumsum(weights) - weights + seq_cost  # weight of each sequence's tile 0
+    return bool(((first // per) != ((first + tiles - 1) // per)).any())
 
 
 class _Workspace:
@@ -789,9 +808,9 @@ def paged_decode_hip(
         flat_seq_cost = int(flat_seq_cost or 0)
     elif num_splits is None:
         # the lengths come to the host in the one sync the reference also makes
-        lens = cache.seq_lens.tolist()
+        lens = cache.seq_lens.to("cpu")
         if seq_lens_host is None:
-            seq_lens_host = torch.tensor(lens, dtype=torch.int32)
+            seq_lens_host = lens.to(torch.int32).contiguous()
         wps = flat_waves_per_simd(cache.kv_dtype, d, None if cache.k_scale is None else cache.k_scale.dtype)
         plan = plan_launch(b, 0, hkv, group, _cu_count(q.device), wps, kv_dtype=cache.kv_dtype,
                            head_dim=d, seq_lens=lens)
@@ -972,7 +991,7 @@ def split_reduce(
 
 def split_count_for(cache: PagedKVCache, device: torch.device) -> int:
     """The classic split count `plan_num_splits` gives this batch."""
-    return plan_num_splits(cache.seq_lens.tolist(), cache.shape.num_kv_heads, cache.shape.gqa_group,
+    return plan_num_splits(cache.seq_lens.to("cpu"), cache.shape.num_kv_heads, cache.shape.gqa_group,
                            _cu_count(device))[0]
 
 

@@ -340,7 +340,62 @@ def test_host_seq_lens_reads_cpu_copies_only():
     assert vb._host_seq_lens(types.SimpleNamespace(), 2) is None
     assert vb._host_seq_lens(types.SimpleNamespace(seq_lens_cpu=None), 2) is None
     m = types.SimpleNamespace(seq_lens_cpu=torch.tensor([5, 6, 7], dtype=torch.int32))
-    assert vb._host_seq_lens(m, 2) == [5, 6]
+    got = vb._host_seq_lens(m, 2)
+    assert got.dtype == torch.int32 and got.is_contiguous() and got.tolist() == [5, 6]
+    m = types.SimpleNamespace(seq_lens_cpu=torch.tensor([5, 6, 7], dtype=torch.int64))
+    assert vb._host_seq_lens(m, 3).dtype == torch.int32
+
+
+def test_host_seq_lens_check_catches_a_stale_copy(monkeypatch):
+    """PAGEDATTN_CHECK_HOST_LENS=1 compares the host copy with seq_lens."""
+    monkeypatch.setenv("PAGEDATTN_CHECK_HOST_LENS", "1")
+    dev = torch.tensor([5, 6, 7], dtype=torch.int32)
+    ok = types.SimpleNamespace(seq_lens=dev, seq_lens_cpu=dev.clone())
+    assert vb._host_seq_lens(ok, 3).tolist() == [5, 6, 7]
+    stale = types.SimpleNamespace(seq_lens=dev, seq_lens_cpu=torch.tensor([5, 6, 8], dtype=torch.int32))
+    with pytest.raises(ValueError, match="stale"):
+        vb._host_seq_lens(stale, 3)
+    monkeypatch.delenv("PAGEDATTN_CHECK_HOST_LENS")
+    assert vb._host_seq_lens(stale, 3).tolist() == [5, 6, 8]  # unchecked by default
+
+
+def test_decode_step_is_planned_once_for_all_layers(monkeypatch):
+    """A step's layers share its metadata: the plan is made for the first
+    layer and reused by the others; a new step (new metadata) plans again.
+    Planning a ragged batch of 256 on host lengths takes well under a
+    millisecond (a loop per length took ~0.4 ms)."""
+    import time
+
+    monkeypatch.setattr(vb, "_cu_count", lambda dev: 256)
+    monkeypatch.setattr(vb, "flat_waves_per_simd", lambda kv_dtype, d: 1)
+    planned = []
+    real = vb.plan_launch
+    monkeypatch.setattr(vb, "plan_launch", lambda *a, **k: planned.append(1) or real(*a, **k))
+    seen = []
+
+    def fake_decode(q, cache, out, sm_scale, **kw):
+        seen.append(kw)
+
+    impl = FakeBaseImpl(num_heads=32, num_kv_heads=8, head_size=128)
+    impl.kv_sharing_target_layer_name = "shared"
+    g = torch.Generator().manual_seed(3)
+    n = 256
+    q = torch.zeros(n, 32, 128, dtype=torch.float16)
+    kvc = torch.zeros((2, 4, 16, 8, 128), dtype=torch.float16)
+    for step in range(3):
+        t = torch.randint(1, 2048, (n,), generator=g, dtype=torch.int32)
+        meta = _meta(num_actual_tokens=n, max_seq_len=int(t.max()), block_table=torch.zeros((n, 4), dtype=torch.int32),
+                     seq_lens=t, seq_lens_cpu=t.clone())
+        for layer in range(24):
+            vb.decode_forward(impl, None, q, q, q, kvc, meta, torch.zeros_like(q), decode=fake_decode)
+        assert len(planned) == step + 1
+        assert all(kw == seen[-1] for kw in seen[-24:])
+        assert torch.equal(seen[-1]["seq_lens_host"], t)
+    lens = torch.randint(1, 2048, (n,), generator=g, dtype=torch.int32)
+    t0 = time.perf_counter()
+    for _ in range(20):
+        real(n, 0, 8, 4, 256, 1, kv_dtype="fp16", head_dim=128, seq_lens=lens)
+    assert (time.perf_counter() - t0) / 20 < 1e-3
 
 
 class _NHDBackend:
