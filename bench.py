@@ -785,6 +785,99 @@ def measure(cfg: str, args, dev, cpu: bool) -> dict:
     return res
 
 
+def _build_inputs(wl, shape, dev, copies_arg=None):
+    """The workload's cache (GPU-filled, seeded), its rotated pool copies and q."""
+    import torch
+
+    from pagedattn import allocate
+
+    used = sum(-(-t // 16) for t in wl.lens)
+    sdt = torch.float32 if wl.scale_fp32 else torch.float16
+    cache = allocate(shape, wl.batch, wl.lens, block_size=16, kv_dtype=wl.kv_dtype, device="cuda",
+                     seed=wl.seed, slack_blocks=wl.pool_blocks - used, scale_dtype=sdt, fill_device="cuda")
+    g = torch.Generator().manual_seed(100 + wl.seed)
+    q = torch.randn((wl.batch, shape.num_q_heads, shape.head_dim), dtype=torch.float16, generator=g).to(dev)
+    pool_bytes = 2 * cache.k_cache.numel() * cache.k_cache.element_size()
+    copies = copies_arg or max(1, math.ceil(512e6 / pool_bytes) + 1)
+    caches = [cache] + [dataclasses.replace(
+        cache, k_cache=cache.k_cache.clone(), v_cache=cache.v_cache.clone(),
+        k_scale=None if cache.k_scale is None else cache.k_scale.clone(),
+        v_scale=None if cache.v_scale is None else cache.v_scale.clone()) for _ in range(copies - 1)]
+    return cache, caches, q, sdt
+
+
+def plan_check(args, dev) -> int:
+    """Re-validate the launch planner on this GPU: for every BASELINE config,
+    time the planner's launch against the other launch shapes (the flat
+    split at the planner's range count, the per-sequence split, unsplit, and
+    the flat split at half and twice the range count), each as an eager
+    whole call (mean of --steps calls, rotating pool copies, flat launches
+    with host lengths) and as a replayed HIP graph (median of replays). One
+    JSON line per config; `margin_pct` is how much slower the fastest
+    alternative is than the planner's choice (negative: an alternative won)."""
+    import torch
+
+    from pagedattn import flat_waves_per_simd, plan_launch, plan_num_splits, pick_num_splits
+    from pagedattn.hip_decode import (RAGGED_FLAT_SEQ_COST, RAGGED_FLAT_SEQ_COST_KV, _cu_count,
+                                      _nearly_uniform, flat_splits_for, paged_decode_hip)
+
+    cfgs = [args.config] if args.config else ["c1", "c2", "c3", "c4", "c5"]
+    for cfg in cfgs:
+        wl = make_workload(cfg)
+        shape = shape_of(wl.shape_name)
+        cache, caches, q, sdt = _build_inputs(wl, shape, dev, args.copies)
+        copies = len(caches)
+        cus = _cu_count(dev)
+        wps = flat_waves_per_simd(wl.kv_dtype, shape.head_dim, sdt)
+        plan = plan_launch(wl.batch, 0, shape.num_kv_heads, shape.gqa_group, cus, wps, kv_dtype=wl.kv_dtype,
+                           head_dim=shape.head_dim, seq_lens=wl.lens)
+        flat = flat_splits_for(shape.num_kv_heads, shape.gqa_group, cus, wps, wl.kv_dtype)
+        cost = 0 if _nearly_uniform(wl.lens) else RAGGED_FLAT_SEQ_COST_KV.get(wl.kv_dtype, RAGGED_FLAT_SEQ_COST)
+        split = plan_num_splits(wl.lens, shape.num_kv_heads, shape.gqa_group, cus)[0]
+        if split < 2:
+            split = max(2, pick_num_splits(wl.batch, shape.num_kv_heads, max(wl.lens), cus))
+        msl = max(wl.lens)
+        variants = {
+            "planned": plan.launch_kwargs(),
+            f"flat F={flat}": {"flat_splits": flat, "flat_seq_cost": cost},
+            f"flat F={max(1, flat // 2)}": {"flat_splits": max(1, flat // 2), "flat_seq_cost": cost},
+            f"flat F={2 * flat}": {"flat_splits": 2 * flat, "flat_seq_cost": cost},
+            f"split S={split}": {"num_splits": split, "max_seq_len": msl},
+            "unsplit": {"num_splits": 1, "max_seq_len": msl},
+        }
+        host = torch.tensor(wl.lens, dtype=torch.int32)
+        out = torch.empty_like(q)
+        res = {}
+        for name, kw in variants.items():
+            kw = dict(kw)
+            if kw.get("flat_splits"):
+                kw["seq_lens_host"] = host
+            step = lambda i, kw=kw: paged_decode_hip(q, caches[i % copies], out=out, **kw)
+            settle(step)
+            for i in range(args.warmup):
+                step(i)
+            eager = statistics.median(_loop_us(step, args.steps, 3))
+            kw_graph = {k: v for k, v in kw.items() if k != "seq_lens_host"}
+            graph = _graph_us(lambda i, kw=kw_graph: paged_decode_hip(q, caches[i % copies], out=out, **kw))
+            res[name] = {"launch": {k: v for k, v in kw.items() if k != "seq_lens_host"},
+                         "eager_us": round(eager, 2), "graph_us": round(graph, 2)}
+            _log(f"{cfg} {name}: eager {eager:.2f} us, graph {graph:.2f} us")
+        planned = res["planned"]
+        same = [n for n, r in res.items() if n != "planned" and r["launch"] == planned["launch"]]
+        alts = {n: r for n, r in res.items() if n != "planned" and n not in same}
+        line = {"plan_check": cfg, "workload": wl.description, "cus": cus, "planned": planned,
+                "planned_is": same, "alternatives": alts}
+        for kind in ("eager_us", "graph_us"):
+            best = min(alts.items(), key=lambda kv: kv[1][kind])
+            line[f"best_alternative_{kind[:-3]}"] = best[0]
+            line[f"margin_{kind[:-3]}_pct"] = round(100 * (best[1][kind] - planned[kind]) / planned[kind], 2)
+        print(json.dumps(line), flush=True)
+        del caches, cache, q, out
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    return 0
+
+
 def summary(r: dict) -> dict:
     """The compact per-config entry of the JSON line."""
     algo = r["algo"]
@@ -851,6 +944,9 @@ def main() -> int:
                          "into profiles/paged_decode_sq_instruction_counts.md")
     ap.add_argument("--seq-cost", type=int, default=None,
                     help="override the flat split's per-sequence charge in tiles (flat_seq_cost)")
+    ap.add_argument("--plan-check", action="store_true",
+                    help="time the planner's launch against the other launch shapes on every config "
+                         "(or --config), one JSON line per config")
     args = ap.parse_args()
 
     if args.record_traffic:
@@ -875,6 +971,9 @@ def main() -> int:
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+
+    if args.plan_check:
+        return plan_check(args, dev)
 
     if args.op == "write":
         from pagedattn import allocate

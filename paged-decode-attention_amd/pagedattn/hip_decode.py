@@ -583,8 +583,11 @@ def _fill_args(
                                           part_lse.dtype, part_lse.get_device()),
            seq_lens_host is None)
     hit = _ARG_TEMPLATES.get(key)
-    objs = (cache, k, v, bt, sl, ks, vs)
-    if hit is not None and all(r is None or r() is o for r, o in zip(hit[0], objs)):
+    if hit is not None:
+        r = hit[0]
+        hit = hit if (r[0]() is cache and r[1]() is k and r[2]() is v and r[3]() is bt and r[4]() is sl
+                      and (ks is None or r[5]() is ks) and (vs is None or r[6]() is vs)) else None
+    if hit is not None:
         if seq_lens_host is not None and flat_splits > 0:
             _check_host_lens(seq_lens_host, q.shape[0])
         a = _abi.PaDecodeArgs.from_buffer_copy(hit[1])
@@ -600,7 +603,7 @@ def _fill_args(
                       flat_splits, flat_seq_cost, seq_lens_host)
     if len(_ARG_TEMPLATES) >= _ARG_TEMPLATES_MAX:
         _ARG_TEMPLATES.clear()
-    refs = tuple(None if o is None else weakref.ref(o) for o in objs)
+    refs = tuple(None if o is None else weakref.ref(o) for o in (cache, k, v, bt, sl, ks, vs))
     _ARG_TEMPLATES[key] = (refs, tmpl)
     return _abi.PaDecodeArgs.from_buffer_copy(tmpl)
 
