@@ -403,9 +403,11 @@ def record_trace(cfg: str, stats_csv: str, trace_csv: str, bench_out: str) -> in
     """Summarise a `rocprofv3 --kernel-trace --stats` run of `bench.py
     --config cfg` into profiles/paged_decode_<cfg>_kernel_trace.md: the top
     kernels, the bench line the same run printed, and the decode kernel's
-    rocprof average over the bench's kernel-alone loop (the longest run of
-    decode dispatches with no merge between them, its last --steps ones)
-    beside the bench's HIP-event figure. Runs on the CPU."""
+    rocprof durations over the bench's two kernel-alone loops (the eager one,
+    its last --steps dispatches, and the replayed graph, its last
+    GRAPH_CALLS x GRAPH_REPLAYS dispatches; the bench brackets both with
+    phase-marker kernels) beside the bench's HIP-event figures. Runs on the
+    CPU."""
     import csv
     import statistics
 
@@ -419,17 +421,12 @@ def record_trace(cfg: str, stats_csv: str, trace_csv: str, bench_out: str) -> in
         trace = [(int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]) for r in csv.DictReader(f)]
     trace.sort()
     kernel = bench["roofline"]["kernel"]
-    runs, cur = [], []
-    for t0, t1, name in trace:
-        if kernel + "<" in name:
-            cur.append((t1 - t0) / 1e3)
-        elif "split_reduce_kernel" in name or "merge_table_kernel" in name or "paged_decode" in name:
-            if cur:
-                runs.append(cur)
-            cur = []
-    if cur:
-        runs.append(cur)
-    alone = max(runs, key=len)[-steps:]
+    marks = [i for i, (_, _, name) in enumerate(trace) if "spin_kernel" in name]
+    if len(marks) < 3:
+        raise SystemExit(f"{trace_csv}: {len(marks)} phase markers (spin_kernel), need 3")
+    between = lambda a, b: [(t1 - t0) / 1e3 for t0, t1, name in trace[a + 1:b] if kernel + "<" in name]
+    alone = between(marks[0], marks[1])[-steps:]
+    graph = between(marks[1], marks[2])[-GRAPH_CALLS * GRAPH_REPLAYS:]
     short = lambda n: n.replace("(anonymous namespace)::", "").split("(")[0].replace("void ", "")[:90]
     cmd = (f"cd /root/repo && export TMPDIR=/tmp && rocprofv3 --kernel-trace --stats -d gpurun_out/trace_{cfg} "
            f"-o {cfg} --output-format csv -- python3 bench.py --config {cfg} --steps {steps} "
@@ -454,15 +451,22 @@ def record_trace(cfg: str, stats_csv: str, trace_csv: str, bench_out: str) -> in
     for r in stats[:6]:
         lines.append(f"| `{short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
                      f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | {float(r['Percentage']):.1f} |")
-    avg = statistics.fmean(alone)
+    avg, gavg = statistics.fmean(alone), statistics.fmean(graph)
+    roof = bench["roofline"]
     lines += [
         "",
-        f"Agreement: the bench's kernel-alone loop (HIP events over {steps} launches) = "
-        f"{bench['roofline']['kernel_us']:.2f} µs; the same {len(alone)} dispatches in rocprof's trace average "
-        f"{avg:.2f} µs (median {statistics.median(alone):.2f})."
-        + (" That eager loop is host-bound at this size (each launch waits for the Python call that "
-           "makes it; more so under the tracer): rocprof's average is the kernel's own time."
-           if bench["roofline"]["kernel_us"] > 1.2 * avg else ""),
+        f"Agreement, decode kernel `{kernel}` alone: the bench's eager loop (HIP events over {steps} "
+        f"launches) = {roof['kernel_eager_us']:.2f} µs, the same {len(alone)} dispatches in rocprof's trace "
+        f"average {avg:.2f} µs (median {statistics.median(alone):.2f}, min {min(alone):.2f}, max "
+        f"{max(alone):.2f}); the bench's replayed graph = {roof['kernel_graph_us']:.2f} µs, its last "
+        f"{len(graph)} dispatches average {gavg:.2f} µs (median {statistics.median(graph):.2f}). The bench "
+        f"line's roofline uses kernel_us = {roof['kernel_us']:.2f} µs"
+        + (" (the eager loop: the launch takes host launch tables, which a captured launch does not)."
+           if roof["kernel_us"] == roof["kernel_eager_us"] else
+           " (the replayed graph: the eager loop's launches wait for the host at this size).")
+        + (" The eager loop is host-bound: each launch waits for the Python call that makes it, "
+           "more so under the tracer, so its HIP-event figure exceeds the kernel's own time."
+           if roof["kernel_eager_us"] > 1.2 * avg else ""),
         "",
         "The bench line printed by the same run:",
         "",
@@ -473,7 +477,8 @@ def record_trace(cfg: str, stats_csv: str, trace_csv: str, bench_out: str) -> in
     ]
     out = ROOT / "profiles" / f"paged_decode_{cfg}_kernel_trace.md"
     out.write_text("\n".join(lines))
-    _log(f"{cfg}: bench kernel {bench['roofline']['kernel_us']:.2f} us, rocprof {avg:.2f} us; wrote {out.name}")
+    _log(f"{cfg}: bench kernel {roof['kernel_eager_us']:.2f} / {roof['kernel_graph_us']:.2f} us (eager / graph), "
+         f"rocprof {avg:.2f} / {gavg:.2f} us; wrote {out.name}")
     return 0
 
 
@@ -578,6 +583,16 @@ def _graph_us(fn, calls: int = GRAPH_CALLS, reps: int = GRAPH_REPLAYS) -> float:
 
 
 LOOP_REPEATS = 6  # extra timed loops of --steps calls, for the median and range
+
+
+def _phase_marker() -> None:
+    """A tiny kernel (torch's spin kernel) outside every timed region: in a
+    rocprofv3 kernel trace the marker dispatches bracket the kernel-alone
+    loops (eager, then the replayed graph), which `--record-trace` reads."""
+    import torch
+
+    torch.cuda._sleep(100)
+    torch.cuda.synchronize()
 
 
 def _loop_us(step, n: int, repeats: int) -> list[float]:
@@ -712,6 +727,7 @@ def measure(cfg: str, args, dev, cpu: bool) -> dict:
                                          max_seq_len=msl)
     else:
         run = lambda c: paged_decode_hip(q, c, out=out, num_splits=1)
+    _phase_marker()  # a kernel trace finds the kernel-alone loops between markers
     for i in range(args.warmup):
         run(caches[i % copies])
     torch.cuda.synchronize()
@@ -722,6 +738,7 @@ def measure(cfg: str, args, dev, cpu: bool) -> dict:
     torch.cuda.synchronize()
     kern_eager_us = ev0.elapsed_time(ev1) / args.steps * 1e3
     _log(f"decode kernel alone: {kern_eager_us:.1f} us/launch (eager)")
+    _phase_marker()
     # The same launches replayed as a HIP graph, which the host's launch
     # rate cannot slow down (it does at C1, whose kernel takes a few us). A
     # captured flat launch takes no host launch tables (it scans seq_lens),
@@ -730,6 +747,7 @@ def measure(cfg: str, args, dev, cpu: bool) -> dict:
     # keeps ahead of the GPU.
     kern_graph_us = _graph_us(lambda i: run(caches[i % copies]))
     _log(f"decode kernel alone: {kern_graph_us:.1f} us/launch (HIP graph)")
+    _phase_marker()
     kern_us = kern_eager_us if host is not None else kern_graph_us
 
     # The merge pass alone. It is a few microseconds of GPU work, less than
