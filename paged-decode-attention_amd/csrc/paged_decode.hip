@@ -1606,10 +1606,15 @@ __global__ void __launch_bounds__(kMergeWaves * 64) split_reduce_kernel(const RP
 // sequences that need it (cut by a range boundary, or empty), so no wave
 // reads seq_lens. Item i: sequence seq[i], its slot count nslot[i] (0 =
 // empty, zeros; up to the flat split count) and its first slot slot[i] =
-// seq[i] + j0. Waves take (item, head) pairs in XCD-contiguous order.
+// seq[i] + j0. The items are grouped by the XCD that ran the decode range
+// j0 (the host computes it from the decode's XCD-contiguous workgroup
+// order), and each group's (item, head) waves run on that XCD, where the
+// partials were written: whole calls 0.2-0.3 us faster at C2-C5 than the
+// plain XCD-contiguous order over the items.
 struct MergeTable {
   RParams r;
   int32_t items;
+  int32_t xstart[9];  // items [xstart[x], xstart[x + 1]) run on XCD x
   uint32_t seq[kHostTab];
   uint32_t nslot[kHostTab];
   uint32_t slot[kHostTab];
@@ -1622,15 +1627,11 @@ __global__ void __launch_bounds__(kMergeWaves * 64) flat_merge_table_kernel(cons
   __shared__ float sw_all[kMergeWaves][kReduceChunk];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  int wg = blockIdx.x;
-  {
-    const int n = gridDim.x, full = n - n % 8;
-    if (wg < full) wg = (wg % 8) * (full / 8) + wg / 8;
-  }
-  const int w = wg * kMergeWaves + wave;
-  if (w >= a.items * p.num_heads) return;
-  const int it = w / p.num_heads;
-  const int h = w % p.num_heads;
+  // workgroup h runs on XCD h % 8 (the hardware deals them round-robin)
+  const int x = blockIdx.x % 8, k = (blockIdx.x / 8) * kMergeWaves + wave;
+  const int it = a.xstart[x] + k / p.num_heads;
+  if (it >= a.xstart[x + 1]) return;
+  const int h = k % p.num_heads;
   const int b = (int)a.seq[it], S = (int)a.nslot[it];
   const int64_t slot0 = a.slot[it];
   merge_into_out<D>(p, p.part_lse + slot0 * p.slb + (int64_t)h * p.slh,
@@ -1926,7 +1927,9 @@ hipError_t launch_reduce(const RParams &rp, int batch, int d, hipStream_t st) {
 }
 
 hipError_t launch_merge_table(const MergeTable &mt, int d, hipStream_t st) {
-  const int grid = (mt.items * mt.r.num_heads + kMergeWaves - 1) / kMergeWaves;
+  int most = 0;
+  for (int x = 0; x < 8; ++x) most = std::max(most, mt.xstart[x + 1] - mt.xstart[x]);
+  const int grid = 8 * ((most * mt.r.num_heads + kMergeWaves - 1) / kMergeWaves);
   const dim3 blk(kMergeWaves * 64);
   switch (d) {
     case 32: hipLaunchKernelGGL((flat_merge_table_kernel<32>), dim3(grid), blk, 0, st, mt); break;
@@ -2028,6 +2031,27 @@ void build_host_plan(const pa_decode_args *a, const KParams &k, HostPlan *hp, Ho
   if (items <= kHostTab) {
     hp->merge_table = true;
     mt.items = items;
+    // XCD of each item: the one holding the flat decode's logical
+    // workgroup of range j0 (unit 0), under the decode's XCD-contiguous order
+    const int units = k.hkv * k.head_tiles;
+    const int grid = (units * F + kFlatWaves - 1) / kFlatWaves, full = grid - grid % 8;
+    int xcd[kHostTab], cnt[8] = {0};
+    for (int i = 0; i < items; ++i) {
+      const int64_t j0 = mt.nslot[i] > 0 ? (int64_t)mt.slot[i] - mt.seq[i] : 0;
+      const int64_t L = (j0 * units) / kFlatWaves;
+      xcd[i] = L < full ? (int)(L / (full / 8)) : (int)(L % 8);
+      ++cnt[xcd[i]];
+    }
+    mt.xstart[0] = 0;
+    for (int x = 0; x < 8; ++x) mt.xstart[x + 1] = mt.xstart[x] + cnt[x];
+    uint32_t s2[kHostTab], n2[kHostTab], o2[kHostTab];
+    int pos[8];
+    for (int x = 0; x < 8; ++x) pos[x] = mt.xstart[x];
+    for (int i = 0; i < items; ++i) {
+      const int q = pos[xcd[i]]++;
+      s2[q] = mt.seq[i]; n2[q] = mt.nslot[i]; o2[q] = mt.slot[i];
+    }
+    for (int i = 0; i < items; ++i) { mt.seq[i] = s2[i]; mt.nslot[i] = n2[i]; mt.slot[i] = o2[i]; }
   }
   if (all != nullptr) all->n_items = items;
 }
