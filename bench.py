@@ -17,9 +17,9 @@ kernel alone, merge alone, HIP-graph whole call, sampled-row parity, bit
 stability, traffic ratio), with C1's CPU baseline on its full 24-row call.
 
 Timing: `us_per_call` (and `value`) is the mean over the --steps timed calls,
-one HIP event pair around them, with a short spin kernel queued just before
-the start event so the pair times back-to-back calls rather than the host's
-first submission to an idle GPU; the same loop is run LOOP_REPEATS more times
+one HIP event pair around them, with one more untimed call queued just before
+the start event (no sync between), so the pair times steady-state calls rather
+than the slow first call after the synchronize; the same loop is run LOOP_REPEATS more times
 for `us_per_call_median` and `us_per_call_range` (median and extremes of the
 loops' means). The decode kernel alone is timed eagerly and as a replayed
 HIP graph; `kernel_us` is the graph figure for launches that take no host
@@ -255,7 +255,7 @@ def bench_write(args, wl, shape, cache, dev) -> int:
         reshape_and_cache(key, value, cache, slots)
     torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    _prime()
+    _prime(lambda: reshape_and_cache(key, value, cache, slots))
     ev0.record()
     for _ in range(args.steps):
         reshape_and_cache(key, value, cache, slots)
@@ -575,7 +575,7 @@ def _graph_us(fn, calls: int = GRAPH_CALLS, reps: int = GRAPH_REPLAYS) -> float:
             fn(i)
     settle(lambda i: graph.replay())
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(2 * reps)]
-    _prime()
+    _prime(graph.replay)
     for r in range(reps):
         evs[2 * r].record()
         graph.replay()
@@ -589,19 +589,15 @@ def _graph_us(fn, calls: int = GRAPH_CALLS, reps: int = GRAPH_REPLAYS) -> float:
 LOOP_REPEATS = 6  # extra timed loops of --steps calls, for the median and range
 
 
-PRIME_CYCLES = 100_000  # spin-kernel cycles queued ahead of a timed loop (~40 us)
-
-
-def _prime() -> None:
-    """Queue a short spin kernel (torch's) on the current stream, no sync.
-    Called right before a timed loop's start event: the GPU is still busy
-    with it when the host records the event and submits the loop's first
-    call, so the event pair times back-to-back calls, as in a serving loop,
-    and not the host's first submission to an idle GPU (that bubble added
-    1.0 us per call to C3's 20-call loop)."""
-    import torch
-
-    torch.cuda._sleep(PRIME_CYCLES)
+def _prime(fn) -> None:
+    """One untimed call of the timed work, queued (no sync) right before a
+    timed loop's start event. The loops follow a synchronize, and the first
+    call after the GPU idles, even briefly, runs slow while the clocks come
+    back: per-call events showed C2's first call at 175-240 us against ~163
+    (C3: up to 88 against ~42), plus the host's first submission to an idle
+    GPU. Queued ahead, that call absorbs both, and the event pair times K
+    calls in steady state, as a serving loop runs them."""
+    fn()
 
 
 def _phase_marker() -> None:
@@ -620,7 +616,7 @@ def _loop_us(step, n: int, repeats: int) -> list[float]:
     import torch
 
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(2 * repeats)]
-    _prime()
+    _prime(lambda: step(0))
     for r in range(repeats):
         evs[2 * r].record()
         for i in range(n):
@@ -719,7 +715,7 @@ def measure(cfg: str, args, dev, cpu: bool) -> dict:
         step(i)
     torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    _prime()
+    _prime(lambda: step(0))
     ev0.record()
     t_wall = time.perf_counter()
     for i in range(args.steps):
@@ -752,7 +748,7 @@ def measure(cfg: str, args, dev, cpu: bool) -> dict:
     for i in range(args.warmup):
         run(caches[i % copies])
     torch.cuda.synchronize()
-    _prime()
+    _prime(lambda: run(caches[0]))
     ev0.record()
     for i in range(args.steps):
         run(caches[i % copies])

@@ -545,11 +545,12 @@ def _ptr(t: torch.Tensor | None) -> int | None:
 
 
 # Validated argument structs, keyed by everything their validation read
-# except the per-call pointers (q, out, workspace, host lengths). The cache
-# object and its tensors enter the key by identity and data pointer and are
-# held by weak references, so a key cannot match a new object that reuses a
-# dead one's id; replacing a tensor or its storage validates again. A tensor
-# reshaped in place on the same memory (resize_, set_) is not noticed.
+# except the per-call pointers (q, out, workspace, host lengths). The cache's
+# tensors enter the key by identity and data pointer and are held by weak
+# references, so a key cannot match a new tensor that reuses a dead one's id;
+# replacing a tensor or its storage validates again (the cache object's other
+# fields enter by value). A tensor reshaped in place on the same memory
+# (resize_, set_) is not noticed.
 _ARG_TEMPLATES: dict[tuple, tuple] = {}
 _ARG_TEMPLATES_MAX = 512
 
@@ -573,7 +574,7 @@ def _fill_args(
     k, v, bt, sl = cache.k_cache, cache.v_cache, cache.block_table, cache.seq_lens
     ks, vs = cache.k_scale, cache.v_scale
     shape = cache.shape
-    key = (id(cache), id(k), k.data_ptr(), id(v), v.data_ptr(), id(bt), bt.data_ptr(), id(sl),
+    key = (id(k), k.data_ptr(), id(v), v.data_ptr(), id(bt), bt.data_ptr(), id(sl),
            sl.data_ptr(), id(ks), 0 if ks is None else ks.data_ptr(), id(vs), 0 if vs is None else vs.data_ptr(),
            cache.kv_dtype, cache.block_size, shape.num_q_heads, shape.num_kv_heads, shape.head_dim,
            q.shape, q.stride(), q.dtype, q.get_device(), out.shape, out.stride(), out.dtype,
@@ -585,8 +586,8 @@ def _fill_args(
     hit = _ARG_TEMPLATES.get(key)
     if hit is not None:
         r = hit[0]
-        hit = hit if (r[0]() is cache and r[1]() is k and r[2]() is v and r[3]() is bt and r[4]() is sl
-                      and (ks is None or r[5]() is ks) and (vs is None or r[6]() is vs)) else None
+        hit = hit if (r[0]() is k and r[1]() is v and r[2]() is bt and r[3]() is sl
+                      and (ks is None or r[4]() is ks) and (vs is None or r[5]() is vs)) else None
     if hit is not None:
         if seq_lens_host is not None and flat_splits > 0:
             _check_host_lens(seq_lens_host, q.shape[0])
@@ -603,7 +604,7 @@ def _fill_args(
                       flat_splits, flat_seq_cost, seq_lens_host)
     if len(_ARG_TEMPLATES) >= _ARG_TEMPLATES_MAX:
         _ARG_TEMPLATES.clear()
-    refs = tuple(None if o is None else weakref.ref(o) for o in (cache, k, v, bt, sl, ks, vs))
+    refs = tuple(None if o is None else weakref.ref(o) for o in (k, v, bt, sl, ks, vs))
     _ARG_TEMPLATES[key] = (refs, tmpl)
     return _abi.PaDecodeArgs.from_buffer_copy(tmpl)
 
@@ -794,12 +795,10 @@ def paged_decode_hip(
     del per_page_bt, num_warps, num_stages
     b, hq, d = q.shape
     shape = cache.shape
-    hkv = shape.num_kv_heads
-    group = shape.gqa_group
     assert d == shape.head_dim
     assert block_n % cache.block_size == 0, "BLOCK_N must be a multiple of the page size"
-    if hq != hkv * group:
-        raise ValueError(f"q has {hq} heads, cache shape expects {hkv * group}")
+    if hq != shape.num_q_heads:
+        raise ValueError(f"q has {hq} heads, cache shape expects {shape.num_q_heads}")
 
     if out is None:
         out = torch.empty((b, hq, d), dtype=q.dtype, device=q.device)
@@ -815,8 +814,8 @@ def paged_decode_hip(
         if seq_lens_host is None:
             seq_lens_host = lens.to(torch.int32).contiguous()
         wps = flat_waves_per_simd(cache.kv_dtype, d, None if cache.k_scale is None else cache.k_scale.dtype)
-        plan = plan_launch(b, 0, hkv, group, _cu_count(q.device), wps, kv_dtype=cache.kv_dtype,
-                           head_dim=d, seq_lens=lens)
+        plan = plan_launch(b, 0, shape.num_kv_heads, shape.gqa_group, _cu_count(q.device), wps,
+                           kv_dtype=cache.kv_dtype, head_dim=d, seq_lens=lens)
         num_splits, flat_splits = plan.num_splits, plan.flat_splits
         if flat_seq_cost is None:
             flat_seq_cost = plan.flat_seq_cost
@@ -826,7 +825,7 @@ def paged_decode_hip(
             merge = flat_needs_merge(lens, flat_splits, cache.block_table.shape[1] * cache.block_size,
                                      int(flat_seq_cost))
     num_splits = int(num_splits)
-    scale = shape.softmax_scale if sm_scale is None else float(sm_scale)
+    scale = d ** -0.5 if sm_scale is None else float(sm_scale)  # shape.softmax_scale
 
     part_out = part_lse = None
     flat = int(flat_splits or 0)
