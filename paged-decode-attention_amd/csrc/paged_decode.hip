@@ -81,6 +81,14 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWaves = 4;          // waves per workgroup (unsplit / classic split)
 constexpr int kFlatWaves = 4;      // flat kernel: one wave per SIMD of a CU
+// Waves per flat-kernel workgroup. int8 caches launch two flat waves per SIMD
+// (their dequantisation keeps one wave busy issuing VALU work), so their
+// workgroup is the CU's eight waves: eight neighbouring kv heads of one range,
+// a whole 1 KB token row of a Llama-shape page read together instead of two
+// 512-byte halves by two workgroups (C4's decode 175.6 -> 172.7 us).
+constexpr int kFlatWavesInt8 = 8;
+template <int KV> constexpr int flat_waves() { return KV == PA_KV_INT8 ? kFlatWavesInt8 : kFlatWaves; }
+inline int flat_waves_of(int kv) { return kv == PA_KV_INT8 ? kFlatWavesInt8 : kFlatWaves; }
 constexpr int kSplitAlign = 32;    // split ranges are multiples of this many tokens
 constexpr float kRescaleLog2 = 8.0f;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -1258,15 +1266,15 @@ struct FlatArgs {
 };
 
 template <int KV, int SC, int D>
-__global__ void __launch_bounds__(kFlatWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ void __launch_bounds__(flat_waves<KV>() * 64) __attribute__((amdgpu_waves_per_eu(2)))
 paged_decode_flat_kernel(const FlatArgs fa) {
   const KParams &p = fa.p;
   using G = Geo<KV, D>;
   static_assert(G::kTT == kSplitAlign, "flat tiles are the kernel's tiles");
-  // the workgroup's waves take 4 neighbouring kv heads of one range, so
-  // together they read a contiguous 4-head stretch of every token row (4
+  // the workgroup's W waves take W neighbouring kv heads of one range, so
+  // together they read a contiguous W-head stretch of every token row (4
   // consecutive ranges of one kv head instead ran 8-14% slower)
-  constexpr int W = kFlatWaves;
+  constexpr int W = flat_waves<KV>();
   __shared__ __attribute__((aligned(16))) uint8_t sm_k[W * G::kKSlotBytes];
   __shared__ __attribute__((aligned(16))) float sm_sc[W][G::kScales];
 
@@ -1767,7 +1775,7 @@ int build_params(const pa_decode_args *a, bool need_partials, KParams *kp) {
     const int64_t seq_tiles_max = ((int64_t)a->max_blocks * a->block_size + kSplitAlign - 1) / kSplitAlign;
     if ((int64_t)a->batch * (seq_tiles_max + a->flat_seq_cost) + a->flat_splits > 0x7fffffff)
       return fail(PA_ERR_UNSUPPORTED, "batch * max tiles per sequence too large for the flat split");
-    if ((int64_t)a->num_kv_heads * head_tiles * a->flat_splits + kFlatWaves > 0x7fffffff)
+    if ((int64_t)a->num_kv_heads * head_tiles * a->flat_splits + kFlatWavesInt8 > 0x7fffffff)
       return fail(PA_ERR_UNSUPPORTED, "flat split grid too large");
   }
 
@@ -1833,7 +1841,7 @@ template <int KV, int SC, int D>
 hipError_t launch_decode_t(const KParams &k, int grid, int mode, hipStream_t st, const HostPlan *hp) {
   const dim3 g(grid), blk(kWaves * 64);
   if (mode == kFlat) {
-    constexpr int W = kFlatWaves;
+    constexpr int W = flat_waves<KV>();
     const int flat_grid = (k.hkv * k.head_tiles * k.flat_splits + W - 1) / W;
     if (hp != nullptr && hp->ranges) {
       hipLaunchKernelGGL((paged_decode_flat_kernel<KV, SC, D>), dim3(flat_grid), dim3(W * 64), 0, st, hp->fa);
@@ -2034,11 +2042,12 @@ void build_host_plan(const pa_decode_args *a, const KParams &k, HostPlan *hp, Ho
     // XCD of each item: the one holding the flat decode's logical
     // workgroup of range j0 (unit 0), under the decode's XCD-contiguous order
     const int units = k.hkv * k.head_tiles;
-    const int grid = (units * F + kFlatWaves - 1) / kFlatWaves, full = grid - grid % 8;
+    const int FW = flat_waves_of(a->kv_dtype);
+    const int grid = (units * F + FW - 1) / FW, full = grid - grid % 8;
     int xcd[kHostTab], cnt[8] = {0};
     for (int i = 0; i < items; ++i) {
       const int64_t j0 = mt.nslot[i] > 0 ? (int64_t)mt.slot[i] - mt.seq[i] : 0;
-      const int64_t L = (j0 * units) / kFlatWaves;
+      const int64_t L = (j0 * units) / FW;
       xcd[i] = L < full ? (int)(L / (full / 8)) : (int)(L % 8);
       ++cnt[xcd[i]];
     }
@@ -2341,9 +2350,10 @@ int pa_flat_waves_per_simd(int kv_dtype, int scale_dtype, int head_dim, int *out
     return fail(PA_ERR_INVALID, "kv_dtype %d / scale_dtype %d is not a supported pair", kv_dtype,
                 scale_dtype);
   int n = 0;
-  const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kFlatWaves * 64, 0);
+  const int FW = flat_waves_of(kv_dtype);
+  const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, FW * 64, 0);
   if (e != hipSuccess) return fail(PA_ERR_HIP, "occupancy query failed: %s", hipGetErrorString(e));
-  *out = n * kFlatWaves / 4;  // workgroups per CU -> waves per SIMD (4 SIMDs per CU)
+  *out = n * FW / 4;  // workgroups per CU -> waves per SIMD (4 SIMDs per CU)
   return ok();
 }
 
