@@ -12,7 +12,7 @@ CPU path.
 
 from __future__ import annotations
 
-import ctypes
+import weakref
 
 import torch
 
@@ -27,6 +27,16 @@ _STORE_DTYPE = {"fp16": torch.float16, "fp8_e5m2": torch.float8_e5m2, "int8": to
 _SCALE_CODE = {torch.float16: _abi.PA_SCALE_FP16, torch.float32: _abi.PA_SCALE_FP32}
 
 
+# Validated argument structs, keyed by everything their validation read
+# except the per-call pointers (key, value, slot_mapping). The cache's tensors
+# enter the key by identity and data pointer and are held by weak references,
+# so a key cannot match a new tensor that reuses a dead one's id. A decode
+# step writes every layer with rows and slots of one geometry, so after the
+# first step each call copies a struct and sets three pointers.
+_WRITE_TEMPLATES: dict[tuple, tuple] = {}
+_WRITE_TEMPLATES_MAX = 512
+
+
 def reshape_and_cache(
     key: torch.Tensor, value: torch.Tensor, cache: PagedKVCache, slot_mapping: torch.Tensor
 ) -> None:
@@ -37,6 +47,33 @@ def reshape_and_cache(
     at or past num_blocks * block_size. For int8 caches the per-(token, head)
     scales are written too. Asynchronous on the current stream.
     """
+    k, v, ks, vs = cache.k_cache, cache.v_cache, cache.k_scale, cache.v_scale
+    tkey = (id(k), k.data_ptr(), id(v), v.data_ptr(), id(ks), 0 if ks is None else ks.data_ptr(), id(vs),
+            0 if vs is None else vs.data_ptr(), cache.kv_dtype, cache.block_size, cache.shape.num_kv_heads,
+            cache.shape.head_dim, key.shape, key.stride(), key.dtype, key.get_device(), value.shape,
+            value.stride(), value.dtype, value.get_device(), slot_mapping.shape, slot_mapping.stride(),
+            slot_mapping.dtype, slot_mapping.get_device())
+    hit = _WRITE_TEMPLATES.get(tkey)
+    if hit is not None:
+        r = hit[0]
+        if (r[0]() is k and r[1]() is v and (ks is None or r[2]() is ks)
+                and (vs is None or r[3]() is vs)):
+            a = _abi.PaCacheWriteArgs.from_buffer_copy(hit[1])
+            a.key, a.value, a.slot_mapping = key.data_ptr(), value.data_ptr(), slot_mapping.data_ptr()
+            _abi.check(_launch(key, _abi.load().pa_cache_write, a), "pa_cache_write")
+            return
+    a = _pack_write_args(key, value, cache, slot_mapping)
+    if len(_WRITE_TEMPLATES) >= _WRITE_TEMPLATES_MAX:
+        _WRITE_TEMPLATES.clear()
+    _WRITE_TEMPLATES[tkey] = (tuple(None if o is None else weakref.ref(o) for o in (k, v, ks, vs)),
+                              _abi.PaCacheWriteArgs.from_buffer_copy(a))
+    _abi.check(_launch(key, _abi.load().pa_cache_write, a), "pa_cache_write")
+
+
+def _pack_write_args(
+    key: torch.Tensor, value: torch.Tensor, cache: PagedKVCache, slot_mapping: torch.Tensor
+) -> _abi.PaCacheWriteArgs:
+    """Validate every tensor of a write and pack pa_cache_write_args."""
     if cache.kv_dtype not in _KV_CODE:
         raise NotImplementedError(f"kv_dtype {cache.kv_dtype!r} is not supported by the HIP writer")
     k, v = cache.k_cache, cache.v_cache
@@ -87,9 +124,7 @@ def reshape_and_cache(
         a.scale_dtype = _SCALE_CODE[ks.dtype]
     else:
         a.scale_dtype = _abi.PA_SCALE_NONE
-    lib = _abi.load()
-    rc = _launch(key, lib.pa_cache_write, a)
-    _abi.check(rc, "pa_cache_write")
+    return a
 
 
 # the vLLM op's name as an alias

@@ -155,3 +155,42 @@ def test_int8_quotients_on_and_next_to_half_integers(scale_dtype):
     assert torch.equal(_raw(c.k_cache.cpu()), _raw(ref.k_cache))
     assert torch.equal(_raw(c.v_cache.cpu()), _raw(ref.v_cache))
     assert torch.equal(c.k_scale.cpu(), ref.k_scale) and torch.equal(c.v_scale.cpu(), ref.v_scale)
+
+
+@pytest.mark.parametrize("kv_dtype", ["fp16", "int8"])
+def test_repeated_writes_through_the_argument_cache(kv_dtype):
+    """Steps of one geometry reuse a validated argument struct with new
+    key/value/slot pointers: every step's bytes equal the oracle's. A cache
+    whose tensors were replaced is validated and written again, and a slot
+    tensor of another dtype is refused even after cached calls."""
+    import dataclasses
+
+    c = allocate(LLAMA3_8B, 2, [64, 40], kv_dtype=kv_dtype, seed=49, device="cuda", slack_blocks=8)
+    ref = _cpu_copy(c)
+    g = torch.Generator().manual_seed(50)
+    nb = c.k_cache.shape[0]
+    perm = torch.randperm(nb * 16, generator=g).to(torch.int64)
+    for step in range(4):
+        key = torch.randn((6, 8, 128), generator=g).half()
+        value = torch.randn((6, 8, 128), generator=g).half()
+        slots = perm[6 * step:6 * step + 6].clone()
+        reshape_and_cache(key.cuda(), value.cuda(), c, slots.cuda())
+        oracle.write_kv(key, value, ref, slots)
+    torch.cuda.synchronize()
+    assert torch.equal(_raw(c.k_cache.cpu()), _raw(ref.k_cache))
+    assert torch.equal(_raw(c.v_cache.cpu()), _raw(ref.v_cache))
+
+    # new tensors in a copy of the cache object: written there, not into c
+    c2 = dataclasses.replace(c, k_cache=c.k_cache.clone(), v_cache=c.v_cache.clone(),
+                             k_scale=None if c.k_scale is None else c.k_scale.clone(),
+                             v_scale=None if c.v_scale is None else c.v_scale.clone())
+    ref2 = _cpu_copy(c2)
+    key = torch.randn((6, 8, 128), generator=g).half()
+    slots = perm[40:46].clone()
+    reshape_and_cache(key.cuda(), key.cuda(), c2, slots.cuda())
+    oracle.write_kv(key, key, ref2, slots)
+    torch.cuda.synchronize()
+    assert torch.equal(_raw(c2.k_cache.cpu()), _raw(ref2.k_cache))
+    assert torch.equal(_raw(c.k_cache.cpu()), _raw(ref.k_cache))  # c untouched
+    with pytest.raises(ValueError, match="int64"):
+        reshape_and_cache(key.cuda(), key.cuda(), c2, slots.to(torch.int32).cuda())
