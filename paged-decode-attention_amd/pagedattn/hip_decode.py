@@ -9,8 +9,8 @@ if the library is missing or the tensors are not on a GPU, the call raises.
 Knobs of the reference that only steer Triton code generation (`per_page_bt`,
 `num_warps`, `num_stages`) are accepted and ignored: the HIP kernels always
 read one block-table entry per 16-token sub-tile (one per page at page size
-16) and size their workgroups themselves (4 waves; the flat kernel's are one
-wave per SIMD of a CU). `block_n` keeps the reference's check that it is a multiple of
+16) and size their workgroups themselves (4 waves; the flat kernel's are the
+CU's four SIMDs, one wave each, or two each for int8 caches). `block_n` keeps the reference's check that it is a multiple of
 the page size; split ranges are aligned to the kernels' 32-token tile.
 """
 
