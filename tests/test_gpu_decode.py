@@ -323,3 +323,35 @@ def test_bf16_split_reduce_output():
     po, pl = decode_partials(q, c, 4)
     out = split_reduce(po, pl, torch.empty((2, 32, 128), dtype=torch.bfloat16, device="cuda"))
     _check_bf16(out, oracle.reference_decode(q, c, out_dtype=torch.float32))
+
+
+@pytest.mark.parametrize("block_size", [128, 256])
+@pytest.mark.parametrize("kv_dtype,scale_dtype", [("fp16", torch.float16), ("bf16", torch.float16),
+                                                  ("fp8_e5m2", torch.float16), ("int8", torch.float16),
+                                                  ("int8", torch.float32)])
+@pytest.mark.parametrize("shape", [LLAMA3_8B, ModelShape(12, 2, 64, "g6-d64")], ids=["llama3-8b", "g6-d64"])
+def test_large_pages_every_kv_dtype_and_launch(block_size, kv_dtype, scale_dtype, shape):
+    """Pages of 128 and 256 tokens (several 32-token tiles per page, so a
+    tile's two 16-row sub-tiles share one block-table entry) for every KV
+    type, through the unsplit, classic split and flat launches (with and
+    without host lengths). At 2 kv heads a flat workgroup spans several
+    ranges (4 per workgroup for int8, 2 otherwise)."""
+    lens = [700, 1, 0, 2 * block_size + 5, 257]
+    c = allocate(shape, len(lens), lens, block_size=block_size, kv_dtype=kv_dtype, seed=11,
+                 scale_dtype=scale_dtype, device="cuda")
+    q = seeded_q(len(lens), shape.num_q_heads, shape.head_dim, 11, device="cuda")
+    ref = oracle.reference_decode(q, c, out_dtype=torch.float32)
+    host = torch.tensor(lens, dtype=torch.int32)
+    live = [i for i, t in enumerate(lens) if t > 0]
+
+    def check(got):
+        # the oracle's empty row is 0/0; the kernels write zeros there
+        _check(got[live], ref[live])
+        assert torch.equal(got[2].float().cpu(), torch.zeros(shape.num_q_heads, shape.head_dim))
+
+    bn = block_size  # the reference's BLOCK_N check: a multiple of the page size
+    check(paged_decode_hip(q, c, block_n=bn, num_splits=1))
+    check(paged_decode_hip(q, c, block_n=bn, num_splits=3, max_seq_len=max(lens)))
+    for f in (1, 7, 64):
+        check(paged_decode_hip(q, c, block_n=bn, flat_splits=f))
+        check(paged_decode_hip(q, c, block_n=bn, flat_splits=f, flat_seq_cost=2, seq_lens_host=host))
