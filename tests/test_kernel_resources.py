@@ -8,8 +8,9 @@ and spill no vector register: a private segment makes every launch set up
 scratch memory, and a spill to it puts memory traffic in the tile loop.
 Scalar registers may spill only in the int8 flat-split instances, only into
 vector-register lanes (v_writelane / v_readlane, no memory), and only a few:
-the variant that spilled none scheduled C4's tile 2.5% slower. CPU only
-(hipcc cross-compiles).
+the variant that spilled none scheduled C4's tile 2.5% slower, and the SIMD
+pair's progress exchange (a few more spilled scalars) made C4's decode 2.3%
+faster. CPU only (hipcc cross-compiles).
 """
 
 from __future__ import annotations
@@ -26,8 +27,8 @@ import pytest
 ROOT = pathlib.Path(__file__).resolve().parent.parent
 PKG = ROOT / "paged-decode-attention_amd"
 # scalar registers an int8 flat instance may spill into vector lanes (the
-# compiler reports 4-14 for the current sources)
-MAX_INT8_SGPR_SPILLS = 16
+# compiler reports 2-19 for the current sources)
+MAX_INT8_SGPR_SPILLS = 24
 
 
 def _build_module():
