@@ -10,8 +10,9 @@ Knobs of the reference that only steer Triton code generation (`per_page_bt`,
 `num_warps`, `num_stages`) are accepted and ignored: the HIP kernels always
 read one block-table entry per 16-token sub-tile (one per page at page size
 16) and size their workgroups themselves (4 waves; the flat kernel's are the
-CU's four SIMDs, one wave each, or two each for int8 caches). `block_n` keeps the reference's check that it is a multiple of
-the page size; split ranges are aligned to the kernels' 32-token tile.
+CU's four SIMDs, one wave each, or two each for int8 caches). `block_n`
+keeps the reference's check that it is a multiple of the page size; split
+ranges are aligned to the kernels' 32-token tile.
 """
 
 from __future__ import annotations
@@ -58,11 +59,13 @@ RAGGED_SPLIT_MIN_TILES = 32
 
 # Flat split: one round of waves, at most FLAT_WAVES_PER_SIMD per SIMD even
 # where the registers allow more. One streaming wave per SIMD measured
-# fastest on every benchmark config with a split (C2-C5): with two, each SIMD's older wave
-# runs ahead and the younger ones form a tail (C2 158.5 us at 1, 159.6 at 2;
-# C3 39.3 and 40.6; C5 312.7 and 316.5; three per SIMD or a second round is
-# slower still). Used when each wave gets at least MIN_FLAT_TILES_PER_WAVE
-# 32-token tiles; smaller batches are latency-bound and run faster unsplit.
+# fastest on every benchmark config with a split (C2-C5): with two, each
+# SIMD's older wave runs ahead and the younger ones form a tail (C2 158.5 us
+# at 1, 159.6 at 2; C3 39.3 and 40.6; C5 312.7 and 316.5); three per SIMD or
+# a second round is slower still, and so are two per SIMD whose pairs
+# balance their progress as int8's do (C2 163.7 against 160.2). Used when
+# each wave gets at least MIN_FLAT_TILES_PER_WAVE 32-token tiles; smaller
+# batches are latency-bound and run faster unsplit.
 FLAT_WAVES_PER_SIMD = 1
 # int8 tiles carry a dequantisation per K and V element (the reference's
 # fp16(x * s)), which keeps one wave per SIMD busy issuing VALU work: a
@@ -101,6 +104,17 @@ SINGLE_SEQ_SPLIT_MAX_TILES = 2048
 # 134 MB. (At 256 CUs: 512 MB, 192 MB and 96 MB.)
 UNSPLIT_MAX_KV_BYTES_PER_CU = {"fp16": 2 << 20, "bf16": 2 << 20, "fp8_e5m2": 768 << 10,
                                "int8": 384 << 10}
+# Rows shorter than UNSPLIT_MIN_ROW_BYTES (head_dim x element size: 1-byte
+# KV at head_dim 64) stream slowly through the unsplit kernel, so there the
+# limit is UNSPLIT_MAX_SHORT_ROW_BYTES_PER_CU. Whole calls at the
+# Qwen2.5-0.5B shape (14 q / 2 kv heads, D = 64, 256 CUs), unsplit against
+# flat (F = 512; int8 F = 1024): fp8 B = 128, T = 1024 (34 MB) 13.6 / 15.1
+# us, B = 128, T = 2048 (67 MB) 23.8 / 20.1, B = 256, T = 1024 23.8 / 20.9,
+# B = 256, T = 2048 (134 MB) 44.3 / 31.8; int8 B = 128, T = 1024 15.4 /
+# 17.1, B = 256, T = 1024 26.2 / 24.1; fp16 (128-byte rows) B = 256,
+# T = 2048 45.0 / 48.5.
+UNSPLIT_MIN_ROW_BYTES = 128
+UNSPLIT_MAX_SHORT_ROW_BYTES_PER_CU = 192 << 10
 # Batches of short sequences that fill the CUs run unsplit, whatever their
 # size and merge or not: the flat split loses there, because its waves
 # switch sequences every few tiles. Per KV type, the longest sequence of a
@@ -332,8 +346,10 @@ def plan_launch(batch: int, max_seq_len: int, num_kv_heads: int, group: int, sm_
             (`short_batch_runs_unsplit`; the nearly-uniform limit only with
             known lengths);
           - a nearly uniform batch (known lengths) that fills the CUs
-            unsplit, with at most UNSPLIT_MAX_KV_BYTES_PER_CU x CUs of K/V,
-            unless the flat split needs no merge either (`flat_needs_merge`);
+            unsplit, with at most UNSPLIT_MAX_KV_BYTES_PER_CU x CUs of K/V
+            (UNSPLIT_MAX_SHORT_ROW_BYTES_PER_CU for rows under
+            UNSPLIT_MIN_ROW_BYTES), unless the flat split needs no merge
+            either (`flat_needs_merge`);
       * otherwise the classic split (`plan_num_splits`), on the known
         lengths or on `batch` sequences of `max_seq_len` tokens.
     A flat plan charges each sequence RAGGED_FLAT_SEQ_COST tiles
@@ -364,7 +380,10 @@ def plan_launch(batch: int, max_seq_len: int, num_kv_heads: int, group: int, sm_
                 return LaunchPlan(1, tmax, 0)
             kv_bytes = int(lens.sum()) * num_kv_heads * head_dim * _KV_ELEM_BYTES.get(kv_dtype, 2) * 2 \
                 if known else 0
-            limit = UNSPLIT_MAX_KV_BYTES_PER_CU.get(kv_dtype, 0) * cus
+            limit = UNSPLIT_MAX_KV_BYTES_PER_CU.get(kv_dtype, 0)
+            if head_dim * _KV_ELEM_BYTES.get(kv_dtype, 2) < UNSPLIT_MIN_ROW_BYTES:
+                limit = min(limit, UNSPLIT_MAX_SHORT_ROW_BYTES_PER_CU)
+            limit *= cus
             if fills and kv_bytes <= limit and merge:
                 return LaunchPlan(1, tmax, 0)
         return LaunchPlan(1, tmax, flat, merge, cost)

@@ -401,6 +401,14 @@ def test_flat_splits_for_and_plan_decode():
     assert plan_decode([1024] * 64, 8, 4, 256, 1, kv_dtype="bf16", head_dim=128) == (1, 1024, 0)
     assert plan_decode([1024] * 64, 8, 4, 256, 1, kv_dtype="fp8_e5m2", head_dim=128) == (1, 1024, 0)
     assert plan_decode([512] * 64, 8, 4, 256, 1, kv_dtype="int8", head_dim=128) == (1, 512, 0)
+    # ... with a lower limit for short 1-byte rows (head_dim 64), which stream
+    # faster flat (Qwen2.5-0.5B shape, 2 kv heads, group 7): 34 MB unsplit,
+    # 67 MB flat
+    assert plan_decode([1024] * 128, 2, 7, 256, 1, kv_dtype="fp8_e5m2", head_dim=64) == (1, 1024, 0)
+    assert plan_decode([2048] * 128, 2, 7, 256, 1, kv_dtype="fp8_e5m2", head_dim=64)[2] == 512
+    assert plan_decode([1024] * 128, 2, 7, 256, 2, kv_dtype="int8", head_dim=64) == (1, 1024, 0)
+    assert plan_decode([1024] * 256, 2, 7, 256, 2, kv_dtype="int8", head_dim=64)[2] == 1024
+    assert plan_decode([2048] * 128, 2, 7, 256, 1, kv_dtype="fp16", head_dim=64) == (1, 2048, 0)
     # ... and above the per-type byte limit takes the flat split
     assert plan_decode([4096] * 64, 8, 4, 256, 1, kv_dtype="fp16", head_dim=128)[2] == 128
     assert plan_decode([2048] * 64, 8, 4, 256, 1, kv_dtype="fp8_e5m2", head_dim=128)[2] == 128
