@@ -80,7 +80,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWaves = 4;          // waves per workgroup (unsplit / classic split)
-constexpr int kFlatWaves = 4;      // flat kernel: one wave per SIMD of a CU
+constexpr int kFlatWaves = 4;      // flat kernel: one wave per SIMD of a CU (2-byte, fp8)
 // Waves per flat-kernel workgroup. int8 caches launch two flat waves per SIMD
 // (their dequantisation keeps one wave busy issuing VALU work), so their
 // workgroup is the CU's eight waves: eight neighbouring kv heads of one range,
@@ -1246,11 +1246,13 @@ __device__ __forceinline__ void cursor_next(SeqCursor &cur, const ro_i32 *seq_le
   }
 }
 
-// The flat split launches one wave per SIMD. With two, a SIMD's older wave
-// runs ahead of the younger one (per-wave timestamps: the younger finish up
-// to 20% later), and that tail costs more than the second wave brings. The
-// register budget is still that of two waves per SIMD, the budget every
-// instance was tuned under.
+// The flat split launches one wave per SIMD for 2-byte and fp8 caches. With
+// two, a SIMD's older wave runs ahead of the younger one (per-wave
+// timestamps: the younger finish up to 20% later), and that tail costs more
+// than the second wave brings. int8 caches, whose tiles keep one wave busy
+// issuing VALU work, launch two per SIMD and balance each pair through LDS
+// (in the kernel below). The register budget is that of two waves per SIMD
+// for every instance, the budget they were tuned under.
 // The flat kernel's arguments: the parameters and, when the host knows the
 // lengths (ntab = F > 0), each range's first tile (sequence b in the bits
 // from kTabTBits up, tile t below), tile count and the length of b, so that
